@@ -1,0 +1,183 @@
+/*
+ * moe_fp8.h - C ABI of the MI355X (gfx950) fused FP8 block-scale MoE layer.
+ *
+ * The layer is the DeepSeek-V3 routed MoE with the shapes of the MLSys'26
+ * FlashInfer MoE track definition moe_fp8_block_scale_ds_routing_topk8_ng8_kg4_e32_h7168_i2048:
+ * 256 global experts in 8 groups, top-4 groups, top-8 experts, 32 experts local to
+ * this device, hidden size 7168, intermediate size 2048, fp8 e4m3fn operands with
+ * 128-wide block scales, bf16 output.
+ *
+ * Every entry point is stream-ordered on the hipStream_t it is given, performs no
+ * host<->device synchronisation and allocates no memory: all temporaries live in a
+ * caller-owned workspace of moe_fp8_workspace_bytes(T) bytes. Pointers are device
+ * pointers to contiguous row-major buffers. Return value: 0 on success, a negative
+ * MOE_FP8_E* code otherwise (moe_fp8_strerror() gives the text); on error nothing
+ * has been launched.
+ *
+ * Reference interface replaced: run() in kernel.py:562-729 (nikhilnd/mlsys26-flashinfer-moe),
+ * and the stages it calls (kernel.py:624-639 routing, 649-661 dispatch and tile schedule,
+ * 663-693 token pack + GEMM1, 695-729 GEMM2 + finalize).
+ */
+#ifndef MOE_FP8_H_
+#define MOE_FP8_H_
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Layer constants; kernel.py:577-588. */
+#define MOE_FP8_HIDDEN          7168
+#define MOE_FP8_INTER           2048
+#define MOE_FP8_EXPERTS_GLOBAL  256
+#define MOE_FP8_EXPERTS_LOCAL   32
+#define MOE_FP8_TOP_K           8
+#define MOE_FP8_N_GROUP         8
+#define MOE_FP8_TOPK_GROUP      4
+#define MOE_FP8_BLOCK           128
+#define MOE_FP8_H_BLOCKS        (MOE_FP8_HIDDEN / MOE_FP8_BLOCK)       /* 56 */
+#define MOE_FP8_I_BLOCKS        (MOE_FP8_INTER / MOE_FP8_BLOCK)        /* 16 */
+#define MOE_FP8_G1_BLOCKS       (2 * MOE_FP8_INTER / MOE_FP8_BLOCK)    /* 32 */
+
+/* routing_bias element type; kernel.py:595 accepts float32, bfloat16 and float16. */
+#define MOE_FP8_BIAS_F32   0
+#define MOE_FP8_BIAS_BF16  1
+#define MOE_FP8_BIAS_F16   2
+
+/* output element type. The reference copies its fp32 accumulator into the caller's
+ * tensor (kernel.py:729); bf16 is the contract type, fp32 is offered so that an
+ * fp32 destination receives the unrounded sums as it would from the reference. */
+#define MOE_FP8_OUT_BF16   0
+#define MOE_FP8_OUT_F32    1
+
+/* Error codes. */
+#define MOE_FP8_OK                  0
+#define MOE_FP8_EINVAL_POINTER     -1  /* a required pointer is NULL */
+#define MOE_FP8_EINVAL_TOKENS      -2  /* num_tokens < 0 or too large */
+#define MOE_FP8_EWORKSPACE         -3  /* workspace NULL or smaller than moe_fp8_workspace_bytes */
+#define MOE_FP8_EINVAL_BIAS_DTYPE  -4
+#define MOE_FP8_EINVAL_OUT_DTYPE   -5
+#define MOE_FP8_ELAUNCH            -6  /* a HIP launch failed (hipGetLastError) */
+#define MOE_FP8_EDEVICE            -7  /* current device is not gfx950 */
+
+/* Largest num_tokens accepted: keeps every flat index (T*8*7168) inside int64 and
+ * the per-token slot index inside int32. */
+#define MOE_FP8_MAX_TOKENS         (1 << 20)
+
+/* Arguments of one layer call; the tensor contract of kernel.py:563-607. */
+typedef struct moe_fp8_args {
+  const float*   routing_logits;       /* [T, 256] fp32                                  */
+  const void*    routing_bias;         /* [256] fp32 | bf16 | fp16 (routing_bias_dtype)  */
+  int32_t        routing_bias_dtype;   /* MOE_FP8_BIAS_*                                 */
+  const uint8_t* hidden_states;        /* [T, 7168] fp8 e4m3fn                           */
+  const float*   hidden_states_scale;  /* [56, T] fp32, 1x128 block per token            */
+  const uint8_t* gemm1_weights;        /* [32, 4096, 7168] fp8 e4m3fn (gate rows 0..2047, up rows 2048..4095) */
+  const float*   gemm1_weights_scale;  /* [32, 32, 56] fp32, 128x128 blocks              */
+  const uint8_t* gemm2_weights;        /* [32, 7168, 2048] fp8 e4m3fn                    */
+  const float*   gemm2_weights_scale;  /* [32, 56, 16] fp32, 128x128 blocks              */
+  int32_t        num_tokens;           /* T                                              */
+  int32_t        local_expert_offset;  /* experts [offset, offset+32) are local          */
+  float          routed_scaling_factor;
+  void*          output;               /* [T, 7168] bf16 or fp32 (output_dtype)          */
+  int32_t        output_dtype;         /* MOE_FP8_OUT_*                                  */
+} moe_fp8_args;
+
+/* Byte offsets of the intermediate arrays inside the workspace. They are part of
+ * the ABI so that callers and tests can read (or, before a later stage, write) the
+ * intermediates of a call (moe_fp8_layout). N_max = 8*T is the largest possible number of local
+ * (token, expert) assignments.
+ *   topk_ids      int32 [T, 8]      selected global expert ids, selection order      (kernel.py:629)
+ *   topk_weights  fp32  [T, 8]      renormalised, scaled routing weights            (kernel.py:630)
+ *   expert_count  int32 [32]        local assignments per local expert              (kernel.py:357)
+ *   expert_start  int32 [33]        CSR offsets into the sorted arrays              (kernel.py:358-360)
+ *   sorted_token  int32 [N_max]     token of each assignment, grouped by expert,
+ *                                   ascending token inside an expert (deterministic) (kernel.py:364)
+ *   sorted_weight fp32  [N_max]     routing weight of each assignment               (kernel.py:365)
+ *   sorted_slot   int32 [N_max]     flat slot t*8+k of each assignment
+ *   token_nlocal  int32 [T]         number of local assignments of each token
+ *   work_items    int32 [max_items, 4]  GEMM work list (expert, first row, rows, 0)  (kernel.py:384-407)
+ *   counters      int32 [16]        [0] number of work items, [1] N, [2] ticket counter
+ *   act           fp8   [N_max, 2048]    SwiGLU output requantised to e4m3fn          (kernel.py:669)
+ *   act_scale     fp32  [N_max, 16]      its 1x128 block scales, row-major per row   (kernel.py:670)
+ *   partial       fp32  [T*8, 7168]      weighted GEMM2 rows of tokens with more than one local
+ *                                        assignment, indexed by flat slot             (kernel.py:704)
+ */
+typedef struct moe_fp8_layout {
+  size_t total_bytes;
+  size_t topk_ids;
+  size_t topk_weights;
+  size_t expert_count;
+  size_t expert_start;
+  size_t sorted_token;
+  size_t sorted_weight;
+  size_t sorted_slot;
+  size_t token_nlocal;
+  size_t slot_rank;
+  size_t block_count;
+  size_t work_items;
+  size_t counters;
+  size_t act;
+  size_t act_scale;
+  size_t partial;
+  int32_t num_tokens;
+  int32_t max_assignments;   /* N_max = 8*T        */
+  int32_t max_work_items;
+  int32_t route_blocks;      /* routing work-groups */
+  int32_t rows_per_item;     /* GEMM rows (assignments) per work item */
+  int32_t reserved[3];
+} moe_fp8_layout;
+
+/* Workspace size for num_tokens tokens (0 if num_tokens is invalid). */
+size_t moe_fp8_workspace_bytes(int32_t num_tokens);
+
+/* Fills *layout for num_tokens tokens. Returns MOE_FP8_OK or MOE_FP8_EINVAL_*. */
+int moe_fp8_workspace_layout(int32_t num_tokens, moe_fp8_layout* layout);
+
+/* Clears the workspace's control block. A freshly allocated workspace must be passed
+ * through this once before its first use; every later call leaves the control block
+ * cleared again, so one workspace is reusable by successive calls on one stream.
+ * Calls that overlap in time must use different workspaces. No counterpart in the
+ * reference, whose temporaries are freshly zeroed torch tensors (kernel.py:348, 669-670, 704). */
+int moe_fp8_workspace_init(void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* The whole layer: routing, dispatch, GEMM1+SwiGLU+requant, GEMM2+weighted combine.
+ * Replaces run() (kernel.py:562-729). */
+int moe_fp8_run(const moe_fp8_args* args, void* workspace, size_t workspace_bytes,
+                hipStream_t stream);
+
+/* Stage 1: routing and dispatch. Writes topk_ids/topk_weights, the expert histogram,
+ * CSR offsets, sorted permutation and the GEMM work list. With skip_routing != 0 the
+ * routing itself is skipped and topk_ids/topk_weights already in the workspace are
+ * dispatched (routing_logits and routing_bias may then be NULL).
+ * Replaces moe_routing_kernel + build_expert_dispatch + build_tile_schedule
+ * (kernel.py:624-639, 649-661, 327-407). */
+int moe_fp8_route_dispatch(const moe_fp8_args* args, int32_t skip_routing, void* workspace,
+                           size_t workspace_bytes, hipStream_t stream);
+
+/* Stage 2: GEMM1 over the gathered tokens of each local expert, SwiGLU (silu of the
+ * second half times the first half) and requantisation of the result to fp8 with one
+ * scale per row per 128 columns. Reads the dispatch arrays, writes act/act_scale.
+ * Replaces the token pack and moe_gemm1_kernel (kernel.py:663-693, 7-151). */
+int moe_fp8_gemm1(const moe_fp8_args* args, void* workspace, size_t workspace_bytes,
+                  hipStream_t stream);
+
+/* Stage 3: GEMM2 of act against the expert's down projection, weighting by the routing
+ * weight and the deterministic per-token combine into args->output.
+ * Replaces moe_gemm2_kernel and the finalize copy (kernel.py:695-729, 153-250). */
+int moe_fp8_gemm2_combine(const moe_fp8_args* args, void* workspace, size_t workspace_bytes,
+                          hipStream_t stream);
+
+/* Text for a return code. */
+const char* moe_fp8_strerror(int code);
+
+/* Library version string. */
+const char* moe_fp8_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MOE_FP8_H_ */

@@ -1,0 +1,11 @@
+"""MI355X-native fused FP8 block-scale MoE layer (DeepSeek-V3 routing, top-8 of 256
+experts, 32 local experts, H=7168, I=2048) behind the entry point of
+nikhilnd/mlsys26-flashinfer-moe's `run` (kernel.py:562-729).
+
+The directory name contains hyphens, so import it through `load_package()` in
+__graft_entry__.py, which registers it as `mlsys26_flashinfer_moe_amd`.
+"""
+from . import _lib
+from .moe import Workspace, make_args, run, validate, workspace_for
+
+__all__ = ["run", "validate", "make_args", "Workspace", "workspace_for", "_lib"]

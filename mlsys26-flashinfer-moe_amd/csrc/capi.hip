@@ -1,0 +1,233 @@
+// C ABI of libmoe_fp8: argument checks, workspace layout and the launch sequence.
+// run() in kernel.py:562-729 is the interface these entry points replace.
+#include <string.h>
+
+#include "moe_internal.h"
+
+namespace moe {
+
+namespace {
+
+constexpr size_t kAlign = 256;
+inline size_t align_up(size_t x) { return (x + kAlign - 1) & ~(kAlign - 1); }
+
+int check_device() {
+  static int verdict[64] = {0};  // 0 unknown, 1 ok, -1 wrong arch
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return MOE_FP8_EDEVICE;
+  if (dev >= 64) return MOE_FP8_OK;
+  if (verdict[dev] == 0) {
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return MOE_FP8_EDEVICE;
+    verdict[dev] = strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 1 : -1;
+  }
+  return verdict[dev] == 1 ? MOE_FP8_OK : MOE_FP8_EDEVICE;
+}
+
+int check_args(const moe_fp8_args* a, bool need_routing, void* ws, size_t ws_bytes,
+               moe_fp8_layout* L) {
+  if (!a) return MOE_FP8_EINVAL_POINTER;
+  int rc = compute_layout(a->num_tokens, L);
+  if (rc != MOE_FP8_OK) return rc;
+  if (a->num_tokens == 0) return MOE_FP8_OK;
+  if (need_routing && (!a->routing_logits || !a->routing_bias)) return MOE_FP8_EINVAL_POINTER;
+  if (!a->hidden_states || !a->hidden_states_scale || !a->gemm1_weights || !a->gemm1_weights_scale ||
+      !a->gemm2_weights || !a->gemm2_weights_scale || !a->output)
+    return MOE_FP8_EINVAL_POINTER;
+  if (a->routing_bias_dtype < MOE_FP8_BIAS_F32 || a->routing_bias_dtype > MOE_FP8_BIAS_F16)
+    return MOE_FP8_EINVAL_BIAS_DTYPE;
+  if (a->output_dtype != MOE_FP8_OUT_BF16 && a->output_dtype != MOE_FP8_OUT_F32)
+    return MOE_FP8_EINVAL_OUT_DTYPE;
+  if (!ws || ws_bytes < L->total_bytes) return MOE_FP8_EWORKSPACE;
+  return check_device();
+}
+
+template <typename T>
+T* at(void* ws, size_t off) {
+  return reinterpret_cast<T*>(reinterpret_cast<char*>(ws) + off);
+}
+
+RouteParams route_params(const moe_fp8_args* a, const moe_fp8_layout& L, void* ws,
+                         int skip_routing) {
+  RouteParams p;
+  p.logits = a->routing_logits;
+  p.bias = a->routing_bias;
+  p.bias_dtype = a->routing_bias_dtype;
+  p.T = a->num_tokens;
+  p.offset = a->local_expert_offset;
+  p.rsf = a->routed_scaling_factor;
+  p.skip_routing = skip_routing;
+  p.single_pass = a->num_tokens <= kSinglePassTokens;
+  p.nblocks = L.route_blocks;
+  p.rows_per_item = L.rows_per_item;
+  p.max_items = L.max_work_items;
+  p.topk_ids = at<int32_t>(ws, L.topk_ids);
+  p.topk_w = at<float>(ws, L.topk_weights);
+  p.expert_count = at<int32_t>(ws, L.expert_count);
+  p.expert_start = at<int32_t>(ws, L.expert_start);
+  p.sorted_token = at<int32_t>(ws, L.sorted_token);
+  p.sorted_weight = at<float>(ws, L.sorted_weight);
+  p.sorted_slot = at<int32_t>(ws, L.sorted_slot);
+  p.token_nlocal = at<int32_t>(ws, L.token_nlocal);
+  p.slot_rank = at<int32_t>(ws, L.slot_rank);
+  p.block_count = at<int32_t>(ws, L.block_count);
+  p.work_items = at<int32_t>(ws, L.work_items);
+  p.counters = at<int32_t>(ws, L.counters);
+  return p;
+}
+
+GemmParams gemm_params(const moe_fp8_args* a, const moe_fp8_layout& L, void* ws) {
+  GemmParams p;
+  p.hidden = a->hidden_states;
+  p.hidden_scale = a->hidden_states_scale;
+  p.w13 = a->gemm1_weights;
+  p.w13_scale = a->gemm1_weights_scale;
+  p.w2 = a->gemm2_weights;
+  p.w2_scale = a->gemm2_weights_scale;
+  p.T = a->num_tokens;
+  p.max_items = L.max_work_items;
+  p.work_items = at<int32_t>(ws, L.work_items);
+  p.counters = at<int32_t>(ws, L.counters);
+  p.sorted_token = at<int32_t>(ws, L.sorted_token);
+  p.sorted_weight = at<float>(ws, L.sorted_weight);
+  p.sorted_slot = at<int32_t>(ws, L.sorted_slot);
+  p.token_nlocal = at<int32_t>(ws, L.token_nlocal);
+  p.act = at<uint8_t>(ws, L.act);
+  p.act_scale = at<float>(ws, L.act_scale);
+  p.partial = at<float>(ws, L.partial);
+  p.out = a->output;
+  p.out_dtype = a->output_dtype;
+  p.topk_ids = at<int32_t>(ws, L.topk_ids);
+  p.offset = a->local_expert_offset;
+  return p;
+}
+
+}  // namespace
+
+int compute_layout(int32_t T, moe_fp8_layout* out) {
+  if (!out) return MOE_FP8_EINVAL_POINTER;
+  if (T < 0 || T > MOE_FP8_MAX_TOKENS) return MOE_FP8_EINVAL_TOKENS;
+  moe_fp8_layout L;
+  memset(&L, 0, sizeof(L));
+  const size_t t = (size_t)T;
+  const size_t nmax = 8 * t;
+  const int blocks = (T + kRouteTokensPerBlock - 1) / kRouteTokensPerBlock;
+  const int rpi = rows_per_item_for(T);
+  const int max_items = kExpertsLocal + (int)((nmax + rpi - 1) / rpi);
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t o = off;
+    off = align_up(off + bytes);
+    return o;
+  };
+  L.counters = take(kNumCounters * sizeof(int32_t));  // first: moe_fp8_workspace_init clears it
+  L.topk_ids = take(t * kTopK * sizeof(int32_t));
+  L.topk_weights = take(t * kTopK * sizeof(float));
+  L.expert_count = take(kExpertsLocal * sizeof(int32_t));
+  L.expert_start = take((kExpertsLocal + 1) * sizeof(int32_t));
+  L.sorted_token = take(nmax * sizeof(int32_t));
+  L.sorted_weight = take(nmax * sizeof(float));
+  L.sorted_slot = take(nmax * sizeof(int32_t));
+  L.token_nlocal = take(t * sizeof(int32_t));
+  L.slot_rank = take(t * kTopK * sizeof(int32_t));
+  L.block_count = take((size_t)blocks * kExpertsLocal * sizeof(int32_t));
+  L.work_items = take((size_t)max_items * 4 * sizeof(int32_t));
+  L.act = take(nmax * kInter);
+  L.act_scale = take(nmax * kIBlocks * sizeof(float));
+  L.partial = take(t * kTopK * kHidden * sizeof(float));
+  L.total_bytes = off;
+  L.num_tokens = T;
+  L.max_assignments = (int32_t)nmax;
+  L.max_work_items = max_items;
+  L.route_blocks = blocks;
+  L.rows_per_item = rpi;
+  *out = L;
+  return MOE_FP8_OK;
+}
+
+}  // namespace moe
+
+using namespace moe;
+
+extern "C" {
+
+size_t moe_fp8_workspace_bytes(int32_t num_tokens) {
+  moe_fp8_layout L;
+  if (compute_layout(num_tokens, &L) != MOE_FP8_OK) return 0;
+  return L.total_bytes;
+}
+
+int moe_fp8_workspace_layout(int32_t num_tokens, moe_fp8_layout* layout) {
+  return compute_layout(num_tokens, layout);
+}
+
+int moe_fp8_workspace_init(void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  if (!workspace || workspace_bytes < kNumCounters * sizeof(int32_t)) return MOE_FP8_EWORKSPACE;
+  if (hipMemsetAsync(workspace, 0, kNumCounters * sizeof(int32_t), stream) != hipSuccess)
+    return MOE_FP8_ELAUNCH;
+  return MOE_FP8_OK;
+}
+
+int moe_fp8_route_dispatch(const moe_fp8_args* args, int32_t skip_routing, void* workspace,
+                           size_t workspace_bytes, hipStream_t stream) {
+  moe_fp8_layout L;
+  const int rc = check_args(args, !skip_routing, workspace, workspace_bytes, &L);
+  if (rc != MOE_FP8_OK) return rc;
+  if (args->num_tokens == 0) return MOE_FP8_OK;
+  const RouteParams p = route_params(args, L, workspace, skip_routing);
+  return launch_route_dispatch(p, stream) == hipSuccess ? MOE_FP8_OK : MOE_FP8_ELAUNCH;
+}
+
+int moe_fp8_gemm1(const moe_fp8_args* args, void* workspace, size_t workspace_bytes,
+                  hipStream_t stream) {
+  moe_fp8_layout L;
+  const int rc = check_args(args, false, workspace, workspace_bytes, &L);
+  if (rc != MOE_FP8_OK) return rc;
+  if (args->num_tokens == 0) return MOE_FP8_OK;
+  const GemmParams p = gemm_params(args, L, workspace);
+  return launch_gemm1(p, L.rows_per_item, stream) == hipSuccess ? MOE_FP8_OK : MOE_FP8_ELAUNCH;
+}
+
+int moe_fp8_gemm2_combine(const moe_fp8_args* args, void* workspace, size_t workspace_bytes,
+                          hipStream_t stream) {
+  moe_fp8_layout L;
+  const int rc = check_args(args, false, workspace, workspace_bytes, &L);
+  if (rc != MOE_FP8_OK) return rc;
+  if (args->num_tokens == 0) return MOE_FP8_OK;
+  const GemmParams p = gemm_params(args, L, workspace);
+  if (launch_gemm2(p, L.rows_per_item, stream) != hipSuccess) return MOE_FP8_ELAUNCH;
+  return launch_combine(p, stream) == hipSuccess ? MOE_FP8_OK : MOE_FP8_ELAUNCH;
+}
+
+int moe_fp8_run(const moe_fp8_args* args, void* workspace, size_t workspace_bytes,
+                hipStream_t stream) {
+  moe_fp8_layout L;
+  const int rc = check_args(args, true, workspace, workspace_bytes, &L);
+  if (rc != MOE_FP8_OK) return rc;
+  if (args->num_tokens == 0) return MOE_FP8_OK;
+  const RouteParams rp = route_params(args, L, workspace, 0);
+  const GemmParams gp = gemm_params(args, L, workspace);
+  if (launch_route_dispatch(rp, stream) != hipSuccess) return MOE_FP8_ELAUNCH;
+  if (launch_gemm1(gp, L.rows_per_item, stream) != hipSuccess) return MOE_FP8_ELAUNCH;
+  if (launch_gemm2(gp, L.rows_per_item, stream) != hipSuccess) return MOE_FP8_ELAUNCH;
+  if (launch_combine(gp, stream) != hipSuccess) return MOE_FP8_ELAUNCH;
+  return MOE_FP8_OK;
+}
+
+const char* moe_fp8_strerror(int code) {
+  switch (code) {
+    case MOE_FP8_OK: return "success";
+    case MOE_FP8_EINVAL_POINTER: return "a required pointer argument is NULL";
+    case MOE_FP8_EINVAL_TOKENS: return "num_tokens is negative or exceeds MOE_FP8_MAX_TOKENS";
+    case MOE_FP8_EWORKSPACE: return "workspace is NULL or smaller than moe_fp8_workspace_bytes(num_tokens)";
+    case MOE_FP8_EINVAL_BIAS_DTYPE: return "routing_bias_dtype must be MOE_FP8_BIAS_F32, _BF16 or _F16";
+    case MOE_FP8_EINVAL_OUT_DTYPE: return "output_dtype must be MOE_FP8_OUT_BF16 or MOE_FP8_OUT_F32";
+    case MOE_FP8_ELAUNCH: return "a HIP kernel launch failed";
+    case MOE_FP8_EDEVICE: return "the current HIP device is not a gfx950 (MI355X) GPU";
+    default: return "unknown error code";
+  }
+}
+
+const char* moe_fp8_version(void) { return "moe_fp8 0.1.0 gfx950"; }
+
+}  // extern "C"

@@ -1,0 +1,114 @@
+// Internal declarations shared by the HIP translation units of libmoe_fp8.
+//
+// Data layout in HBM (all row-major, contiguous):
+//   caller tensors   : the contract of kernel.py:591-607 (see include/moe_fp8.h)
+//   workspace arrays : moe_fp8_layout offsets; every array is 256-byte aligned.
+// Kernels of one call run in this order on one stream:
+//   route_dispatch_kernel -> [place_kernel] -> gemm1_kernel -> gemm2_kernel -> combine_kernel
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/moe_fp8.h"
+
+namespace moe {
+
+constexpr int kHidden = MOE_FP8_HIDDEN;        // 7168
+constexpr int kInter = MOE_FP8_INTER;          // 2048
+constexpr int kExpertsGlobal = MOE_FP8_EXPERTS_GLOBAL;
+constexpr int kExpertsLocal = MOE_FP8_EXPERTS_LOCAL;
+constexpr int kTopK = MOE_FP8_TOP_K;
+constexpr int kNGroup = MOE_FP8_N_GROUP;
+constexpr int kTopKGroup = MOE_FP8_TOPK_GROUP;
+constexpr int kGroupSize = kExpertsGlobal / kNGroup;  // 32
+constexpr int kBlock = MOE_FP8_BLOCK;          // 128
+constexpr int kHBlocks = MOE_FP8_H_BLOCKS;     // 56
+constexpr int kIBlocks = MOE_FP8_I_BLOCKS;     // 16
+
+// Routing: one wavefront per token, 16 tokens per work-group of 1024 threads.
+constexpr int kRouteTokensPerBlock = 16;
+constexpr int kRouteThreads = 64 * kRouteTokensPerBlock;
+// Up to this many tokens the last routing work-group also places every assignment,
+// so dispatch needs no second launch.
+constexpr int kSinglePassTokens = 256;
+
+// Control block (workspace counters[]).
+constexpr int kCtrItems = 0;    // number of GEMM work items
+constexpr int kCtrAssign = 1;   // N, the number of local assignments
+constexpr int kCtrTicket = 2;   // routing work-groups finished (reset by the last one)
+constexpr int kNumCounters = 16;
+
+// GEMM tiling shared by host and device.
+constexpr int kG1ColsPerBlock = 128;                 // SwiGLU output columns per GEMM1 work-group
+constexpr int kG1ColBlocks = kInter / kG1ColsPerBlock;   // 16
+constexpr int kG2RowsPerBlock = 256;                 // output (hidden) rows per GEMM2 work-group
+constexpr int kG2RowBlocks = kHidden / kG2RowsPerBlock;  // 28
+constexpr int kGemmWaves = 8;
+
+// Rows (assignments) per GEMM work item for a call with T tokens.
+inline int rows_per_item_for(int T) {
+  if (T <= 64) return 16;
+  if (T <= 512) return 32;
+  return 32;
+}
+
+int compute_layout(int32_t T, moe_fp8_layout* out);
+
+// Parameters of the routing/dispatch kernels.
+struct RouteParams {
+  const float* logits;
+  const void* bias;
+  int bias_dtype;
+  int T;
+  int offset;
+  float rsf;
+  int skip_routing;
+  int single_pass;
+  int nblocks;
+  int rows_per_item;
+  int max_items;
+  int32_t* topk_ids;
+  float* topk_w;
+  int32_t* expert_count;
+  int32_t* expert_start;
+  int32_t* sorted_token;
+  float* sorted_weight;
+  int32_t* sorted_slot;
+  int32_t* token_nlocal;
+  int32_t* slot_rank;
+  int32_t* block_count;  // [nblocks, 32], becomes the exclusive prefix over blocks
+  int32_t* work_items;   // [max_items, 4]
+  int32_t* counters;
+};
+
+struct GemmParams {
+  const uint8_t* hidden;       // [T, 7168]
+  const float* hidden_scale;   // [56, T]
+  const uint8_t* w13;          // [32, 4096, 7168]
+  const float* w13_scale;      // [32, 32, 56]
+  const uint8_t* w2;           // [32, 7168, 2048]
+  const float* w2_scale;       // [32, 56, 16]
+  int T;
+  int max_items;
+  const int32_t* work_items;
+  const int32_t* counters;
+  const int32_t* sorted_token;
+  const float* sorted_weight;
+  const int32_t* sorted_slot;
+  const int32_t* token_nlocal;
+  uint8_t* act;                // [N_max, 2048]
+  float* act_scale;            // [N_max, 16]
+  float* partial;              // [T*8, 7168]
+  void* out;                   // [T, 7168]
+  int out_dtype;
+  const int32_t* topk_ids;
+  int offset;
+};
+
+hipError_t launch_route_dispatch(const RouteParams& p, hipStream_t s);
+hipError_t launch_gemm1(const GemmParams& p, int rows_per_item, hipStream_t s);
+hipError_t launch_gemm2(const GemmParams& p, int rows_per_item, hipStream_t s);
+hipError_t launch_combine(const GemmParams& p, hipStream_t s);
+
+}  // namespace moe

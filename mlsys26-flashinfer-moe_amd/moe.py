@@ -1,0 +1,189 @@
+"""Python entry point of the MI355X fused FP8 MoE layer.
+
+`run` has the signature, argument meaning, validation messages and destination-passing
+behaviour of the reference's `run` (kernel.py:562-729). All arithmetic happens in the
+gfx950 HIP library behind the C ABI of include/moe_fp8.h; this module only validates,
+places tensors on the GPU, manages the per-stream workspace and passes raw pointers.
+"""
+from __future__ import annotations
+
+import threading
+
+import torch
+
+from . import _lib
+from ._lib import (BIAS_BF16, BIAS_F16, BIAS_F32, EXPERTS_GLOBAL, EXPERTS_LOCAL, G1_BLOCKS,
+                   H_BLOCKS, HIDDEN, I_BLOCKS, INTER, OUT_BF16, OUT_F32)
+
+_BIAS_CODES = {torch.float32: BIAS_F32, torch.bfloat16: BIAS_BF16, torch.float16: BIAS_F16}
+
+
+def _check_cuda_and_move(t: torch.Tensor, device: torch.device) -> torch.Tensor:
+    """kernel.py:544-549."""
+    if t.device.type == "cuda":
+        return t
+    if device.type != "cuda":
+        raise RuntimeError("CUDA is required to run this kernel; no CUDA device available.")
+    return t.to(device, non_blocking=True)
+
+
+def _ensure_cuda(*tensors) -> torch.device:
+    """kernel.py:552-559 (torch's "cuda" device is the HIP device on ROCm)."""
+    if not torch.cuda.is_available():
+        for t in tensors:
+            if isinstance(t, torch.Tensor) and t.is_cuda:
+                raise RuntimeError("CUDA inputs provided but CUDA is reported unavailable.")
+        raise RuntimeError("CUDA is required to run this kernel; no CUDA device available.")
+    return torch.device("cuda")
+
+
+def validate(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
+             gemm1_weights_scale, gemm2_weights, gemm2_weights_scale) -> int:
+    """The dtype and shape checks of kernel.py:591-607; returns T."""
+    assert hidden_states.dtype == torch.float8_e4m3fn, "hidden_states must be FLOAT8_E4M3FN"
+    assert gemm1_weights.dtype == torch.float8_e4m3fn, "gemm1_weights must be FLOAT8_E4M3FN"
+    assert gemm2_weights.dtype == torch.float8_e4m3fn, "gemm2_weights must be FLOAT8_E4M3FN"
+    assert routing_logits.dtype == torch.float32, "routing_logits must be float32"
+    assert routing_bias.dtype in (torch.float32, torch.bfloat16, torch.float16), \
+        "routing_bias must be float or bf16/fp16"
+    assert hidden_states_scale.dtype == torch.float32, "hidden_states_scale must be float32"
+    assert gemm1_weights_scale.dtype == torch.float32, "gemm1_weights_scale must be float32"
+    assert gemm2_weights_scale.dtype == torch.float32, "gemm2_weights_scale must be float32"
+
+    T = int(routing_logits.shape[0])
+    assert routing_logits.shape[-1] == EXPERTS_GLOBAL, "routing_logits last dim must be 256"
+    assert hidden_states.shape == (T, HIDDEN), "hidden_states must be [T, 7168]"
+    assert hidden_states_scale.shape == (H_BLOCKS, T), "hidden_states_scale must be [56, T]"
+    assert gemm1_weights.shape == (EXPERTS_LOCAL, 2 * INTER, HIDDEN), "gemm1_weights must be [32, 4096, 7168]"
+    assert gemm1_weights_scale.shape == (EXPERTS_LOCAL, G1_BLOCKS, H_BLOCKS), \
+        "gemm1_weights_scale must be [32, 32, 56]"
+    assert gemm2_weights.shape == (EXPERTS_LOCAL, HIDDEN, INTER), "gemm2_weights must be [32, 7168, 2048]"
+    assert gemm2_weights_scale.shape == (EXPERTS_LOCAL, H_BLOCKS, I_BLOCKS), \
+        "gemm2_weights_scale must be [32, 56, 16]"
+    return T
+
+
+class Workspace:
+    """A device workspace for the C ABI, initialised once with moe_fp8_workspace_init.
+
+    The library leaves the control block cleared after every call, so one workspace
+    serves any number of successive calls issued on one stream.
+    """
+
+    def __init__(self, num_tokens: int, device: torch.device, stream: torch.cuda.Stream | None = None):
+        self.layout = _lib.workspace_layout(num_tokens)
+        self.nbytes = int(self.layout.total_bytes)
+        self.buffer = torch.empty(max(self.nbytes, 256), dtype=torch.uint8, device=device)
+        stream = stream or torch.cuda.current_stream(device)
+        _lib.check(_lib.load().moe_fp8_workspace_init(self.buffer.data_ptr(), self.buffer.numel(),
+                                                      stream.cuda_stream), "moe_fp8_workspace_init")
+
+    @property
+    def ptr(self) -> int:
+        return self.buffer.data_ptr()
+
+    def view(self, name: str, dtype: torch.dtype, count: int) -> torch.Tensor:
+        """The workspace array `name` (a moe_fp8_layout field) as a 1-D tensor of `count` items."""
+        off = getattr(self.layout, name)
+        nbytes = count * torch.empty((), dtype=dtype).element_size()
+        return self.buffer[off:off + nbytes].view(dtype)
+
+
+_ws_lock = threading.Lock()
+_ws_cache: dict[tuple[int, int], Workspace] = {}
+
+
+def workspace_for(num_tokens: int, device: torch.device) -> Workspace:
+    """The cached workspace of the current stream on `device`, grown to fit num_tokens."""
+    stream = torch.cuda.current_stream(device)
+    key = (device.index if device.index is not None else torch.cuda.current_device(), stream.cuda_stream)
+    need = _lib.workspace_bytes(num_tokens)
+    with _ws_lock:
+        ws = _ws_cache.get(key)
+        if ws is None or ws.buffer.numel() < need:
+            ws = Workspace(num_tokens, device, stream)
+            _ws_cache[key] = ws
+        elif ws.layout.num_tokens != num_tokens:
+            ws.layout = _lib.workspace_layout(num_tokens)
+            ws.nbytes = int(ws.layout.total_bytes)
+        return ws
+
+
+def make_args(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
+              gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, local_expert_offset,
+              routed_scaling_factor, output) -> _lib.MoeFp8Args:
+    """Packs device tensors into struct moe_fp8_args (pointers only; no copies)."""
+    a = _lib.MoeFp8Args()
+    a.routing_logits = routing_logits.data_ptr() if routing_logits is not None else None
+    a.routing_bias = routing_bias.data_ptr() if routing_bias is not None else None
+    a.routing_bias_dtype = _BIAS_CODES[routing_bias.dtype] if routing_bias is not None else BIAS_F32
+    a.hidden_states = hidden_states.data_ptr()
+    a.hidden_states_scale = hidden_states_scale.data_ptr()
+    a.gemm1_weights = gemm1_weights.data_ptr()
+    a.gemm1_weights_scale = gemm1_weights_scale.data_ptr()
+    a.gemm2_weights = gemm2_weights.data_ptr()
+    a.gemm2_weights_scale = gemm2_weights_scale.data_ptr()
+    a.num_tokens = int(hidden_states.shape[0])
+    a.local_expert_offset = int(local_expert_offset)
+    a.routed_scaling_factor = float(routed_scaling_factor)
+    a.output = output.data_ptr()
+    a.output_dtype = OUT_F32 if output.dtype == torch.float32 else OUT_BF16
+    return a
+
+
+@torch.no_grad()
+def run(
+    routing_logits: torch.Tensor,
+    routing_bias: torch.Tensor,
+    hidden_states: torch.Tensor,
+    hidden_states_scale: torch.Tensor,
+    gemm1_weights: torch.Tensor,
+    gemm1_weights_scale: torch.Tensor,
+    gemm2_weights: torch.Tensor,
+    gemm2_weights_scale: torch.Tensor,
+    local_expert_offset: int,
+    routed_scaling_factor: float,
+    output: torch.Tensor,
+):
+    """The fused FP8 block-scale DeepSeek-V3 MoE layer; writes `output` in place.
+
+    Same contract as kernel.py:562-729: inputs are validated with the reference's
+    assertions, CPU inputs are moved to the GPU, and the result (the local experts'
+    contribution, weighted by the renormalised routing weights) is written into
+    `output` [T, 7168]. A bf16 or fp32 `output` on the GPU is written directly by the
+    kernels; any other dtype or device receives a copy_ of a bf16 result.
+    """
+    T = validate(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
+                 gemm1_weights_scale, gemm2_weights, gemm2_weights_scale)
+    assert tuple(output.shape) == (T, HIDDEN), "output must be [T, 7168]"
+    device = _ensure_cuda(routing_logits, routing_bias, hidden_states, hidden_states_scale,
+                          gemm1_weights, gemm1_weights_scale, gemm2_weights, gemm2_weights_scale)
+    lib = _lib.load()
+
+    logits = _check_cuda_and_move(routing_logits, device).contiguous()
+    bias = _check_cuda_and_move(routing_bias, device).contiguous()
+    hidden = _check_cuda_and_move(hidden_states, device).contiguous()
+    hidden_scale = _check_cuda_and_move(hidden_states_scale, device).contiguous()
+    w13 = _check_cuda_and_move(gemm1_weights, device).contiguous()
+    w13_scale = _check_cuda_and_move(gemm1_weights_scale, device).contiguous()
+    w2 = _check_cuda_and_move(gemm2_weights, device).contiguous()
+    w2_scale = _check_cuda_and_move(gemm2_weights_scale, device).contiguous()
+    dev = logits.device
+    for t in (bias, hidden, hidden_scale, w13, w13_scale, w2, w2_scale):
+        if t.device != dev:
+            raise RuntimeError(f"all inputs must be on one device; got {t.device} and {dev}")
+
+    direct = output.is_cuda and output.device == dev and output.is_contiguous() and \
+        output.dtype in (torch.bfloat16, torch.float32)
+    dst = output if direct else torch.empty((T, HIDDEN), dtype=torch.bfloat16, device=dev)
+    if T == 0:
+        return None
+    with torch.cuda.device(dev):
+        ws = workspace_for(T, dev)
+        args = make_args(logits, bias, hidden, hidden_scale, w13, w13_scale, w2, w2_scale,
+                         local_expert_offset, routed_scaling_factor, dst)
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        _lib.check(lib.moe_fp8_run(args, ws.ptr, ws.buffer.numel(), stream), "moe_fp8_run")
+    if not direct:
+        output.copy_(dst)
+    return None

@@ -1,0 +1,97 @@
+"""Helpers for the GPU parity tests: run the C-ABI stages and read the workspace."""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import torch
+
+import __graft_entry__ as ge
+
+pkg = ge.load_package()
+from mlsys26_flashinfer_moe_amd import _lib, inputs  # noqa: E402
+from mlsys26_flashinfer_moe_amd.moe import Workspace, make_args  # noqa: E402
+
+DUMMY = {}
+
+
+def dummy(dev):
+    """Tiny non-null device buffers standing in for inputs a stage does not read."""
+    if dev not in DUMMY:
+        DUMMY[dev] = dict(
+            hidden=torch.zeros((1, 16), dtype=torch.float8_e4m3fn, device=dev),
+            scale=torch.zeros(16, dtype=torch.float32, device=dev),
+            out=torch.zeros(16, dtype=torch.bfloat16, device=dev),
+        )
+    return DUMMY[dev]
+
+
+def routing_args(logits: torch.Tensor, bias: torch.Tensor, offset: int, rsf: float, hidden=None):
+    d = dummy(logits.device)
+    T = logits.shape[0]
+    h = hidden if hidden is not None else d["hidden"]
+    a = make_args(logits, bias, h, d["scale"], d["hidden"], d["scale"], d["hidden"], d["scale"],
+                  offset, rsf, d["out"])
+    a.num_tokens = T
+    return a
+
+
+def new_workspace(T: int, dev) -> Workspace:
+    return Workspace(T, dev)
+
+
+def stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def route_dispatch(args, ws: Workspace, skip_routing: int = 0):
+    _lib.check(_lib.load().moe_fp8_route_dispatch(args, int(skip_routing), ws.ptr, ws.buffer.numel(), stream()),
+               "moe_fp8_route_dispatch")
+
+
+def gemm1(args, ws: Workspace):
+    _lib.check(_lib.load().moe_fp8_gemm1(args, ws.ptr, ws.buffer.numel(), stream()), "moe_fp8_gemm1")
+
+
+def gemm2_combine(args, ws: Workspace):
+    _lib.check(_lib.load().moe_fp8_gemm2_combine(args, ws.ptr, ws.buffer.numel(), stream()),
+               "moe_fp8_gemm2_combine")
+
+
+def run_layer(args, ws: Workspace):
+    _lib.check(_lib.load().moe_fp8_run(args, ws.ptr, ws.buffer.numel(), stream()), "moe_fp8_run")
+
+
+def read(ws: Workspace, name: str, dtype: torch.dtype, count: int) -> np.ndarray:
+    torch.cuda.synchronize()
+    t = ws.view(name, dtype, count).cpu()
+    if dtype == torch.float8_e4m3fn:
+        t = t.view(torch.uint8)
+    return t.numpy().copy()
+
+
+def write(ws: Workspace, name: str, arr: np.ndarray):
+    src = torch.from_numpy(np.ascontiguousarray(arr))
+    ws.view(name, src.dtype, src.numel()).copy_(src.reshape(-1).to(ws.buffer.device))
+    torch.cuda.synchronize()
+
+
+def counters(ws: Workspace) -> np.ndarray:
+    return read(ws, "counters", torch.int32, 16)
+
+
+def to_numpy_inputs(kw: dict) -> dict:
+    """run() keyword arguments on the GPU -> the oracle's numpy arguments."""
+    u8 = lambda t: t.view(torch.uint8).cpu().numpy()
+    return dict(
+        routing_logits=kw["routing_logits"].cpu().numpy(),
+        routing_bias=kw["routing_bias"].float().cpu().numpy(),
+        hidden_states=u8(kw["hidden_states"]),
+        hidden_states_scale=kw["hidden_states_scale"].cpu().numpy(),
+        gemm1_weights=u8(kw["gemm1_weights"]),
+        gemm1_weights_scale=kw["gemm1_weights_scale"].cpu().numpy(),
+        gemm2_weights=u8(kw["gemm2_weights"]),
+        gemm2_weights_scale=kw["gemm2_weights_scale"].cpu().numpy(),
+        local_expert_offset=kw["local_expert_offset"],
+        routed_scaling_factor=kw["routed_scaling_factor"],
+    )

@@ -1,0 +1,122 @@
+"""CPU-side checks of the C ABI: the library loads, exports every function declared in
+include/moe_fp8.h, computes consistent workspace layouts, and rejects bad arguments
+with the documented codes before touching the GPU."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parent.parent
+
+
+@pytest.fixture(scope="module")
+def lib(pkg):
+    return pkg._lib.load()
+
+
+def test_exports_every_declared_function(pkg, lib):
+    header = (ROOT / "include" / "moe_fp8.h").read_text()
+    declared = set(re.findall(r"^\s*(?:int|size_t|const char\*)\s+(moe_fp8_\w+)\s*\(", header, re.M))
+    assert declared == set(pkg._lib.EXPORTED_SYMBOLS)
+    for name in declared:
+        assert hasattr(lib, name), name
+
+
+def test_constants_match_header(pkg):
+    header = (ROOT / "include" / "moe_fp8.h").read_text()
+    vals = dict(re.findall(r"#define\s+(MOE_FP8_\w+)\s+(-?\d+)\b", header))
+    L = pkg._lib
+    assert int(vals["MOE_FP8_HIDDEN"]) == L.HIDDEN and int(vals["MOE_FP8_INTER"]) == L.INTER
+    assert int(vals["MOE_FP8_EXPERTS_LOCAL"]) == L.EXPERTS_LOCAL
+    for name in ("OK", "EINVAL_POINTER", "EINVAL_TOKENS", "EWORKSPACE", "EINVAL_BIAS_DTYPE",
+                 "EINVAL_OUT_DTYPE", "ELAUNCH", "EDEVICE"):
+        assert int(vals["MOE_FP8_" + name]) == getattr(L, name)
+
+
+def test_struct_sizes(pkg):
+    # 14 fields with natural alignment on x86-64
+    assert ctypes.sizeof(pkg._lib.MoeFp8Args) == 104
+    assert ctypes.sizeof(pkg._lib.MoeFp8Layout) == 16 * 8 + 8 * 4
+
+
+@pytest.mark.parametrize("T", [0, 1, 15, 16, 17, 64, 257, 1024, 4096, 8192, 65536])
+def test_layout_consistent(pkg, T):
+    L = pkg._lib.workspace_layout(T)
+    assert L.num_tokens == T and L.max_assignments == 8 * T
+    assert L.route_blocks == (T + 15) // 16
+    assert L.max_work_items == 32 + (8 * T + L.rows_per_item - 1) // L.rows_per_item
+    assert L.counters == 0
+    arrays = [
+        ("topk_ids", 4 * 8 * T), ("topk_weights", 4 * 8 * T), ("expert_count", 4 * 32),
+        ("expert_start", 4 * 33), ("sorted_token", 4 * 8 * T), ("sorted_weight", 4 * 8 * T),
+        ("sorted_slot", 4 * 8 * T), ("token_nlocal", 4 * T), ("slot_rank", 4 * 8 * T),
+        ("block_count", 4 * 32 * L.route_blocks), ("work_items", 16 * L.max_work_items),
+        ("counters", 64), ("act", 8 * T * 2048), ("act_scale", 4 * 8 * T * 16),
+        ("partial", 4 * 8 * T * 7168),
+    ]
+    spans = sorted((getattr(L, n), getattr(L, n) + b, n) for n, b in arrays)
+    for (a0, a1, an), (b0, b1, bn) in zip(spans, spans[1:]):
+        assert a1 <= b0, f"{an} overlaps {bn}"
+    for off, _, n in spans:
+        assert off % 256 == 0, n
+    assert spans[-1][1] <= L.total_bytes
+    assert pkg._lib.workspace_bytes(T) == L.total_bytes
+
+
+def test_invalid_tokens(pkg, lib):
+    assert lib.moe_fp8_workspace_bytes(-1) == 0
+    assert lib.moe_fp8_workspace_bytes((1 << 20) + 1) == 0
+    lay = pkg._lib.MoeFp8Layout()
+    assert lib.moe_fp8_workspace_layout(-5, ctypes.byref(lay)) == pkg._lib.EINVAL_TOKENS
+
+
+def _args(pkg, T=4):
+    a = pkg._lib.MoeFp8Args()
+    fake = 0x1000
+    for f in ("routing_logits", "routing_bias", "hidden_states", "hidden_states_scale", "gemm1_weights",
+              "gemm1_weights_scale", "gemm2_weights", "gemm2_weights_scale", "output"):
+        setattr(a, f, fake)
+    a.num_tokens = T
+    a.routed_scaling_factor = 2.5
+    return a
+
+
+def test_argument_errors_are_reported_before_any_launch(pkg, lib):
+    L = pkg._lib
+    big = L.workspace_bytes(4)
+    a = _args(pkg)
+    assert lib.moe_fp8_run(None, 0x1000, big, None) == L.EINVAL_POINTER
+    a.hidden_states = None
+    assert lib.moe_fp8_run(ctypes.byref(a), 0x1000, big, None) == L.EINVAL_POINTER
+    a = _args(pkg)
+    a.routing_logits = None
+    assert lib.moe_fp8_run(ctypes.byref(a), 0x1000, big, None) == L.EINVAL_POINTER
+    # ...but dispatch of given top-k lists does not need the router inputs
+    assert lib.moe_fp8_route_dispatch(ctypes.byref(a), 1, 0x1000, big, None) != L.EINVAL_POINTER
+    a = _args(pkg)
+    a.num_tokens = -1
+    assert lib.moe_fp8_run(ctypes.byref(a), 0x1000, big, None) == L.EINVAL_TOKENS
+    a = _args(pkg)
+    assert lib.moe_fp8_run(ctypes.byref(a), 0x1000, big - 1, None) == L.EWORKSPACE
+    assert lib.moe_fp8_run(ctypes.byref(a), None, big, None) == L.EWORKSPACE
+    a.routing_bias_dtype = 3
+    assert lib.moe_fp8_run(ctypes.byref(a), 0x1000, big, None) == L.EINVAL_BIAS_DTYPE
+    a = _args(pkg)
+    a.output_dtype = 2
+    assert lib.moe_fp8_gemm2_combine(ctypes.byref(a), 0x1000, big, None) == L.EINVAL_OUT_DTYPE
+    # T = 0 is a no-op that succeeds without a device
+    a = _args(pkg, 0)
+    assert lib.moe_fp8_run(ctypes.byref(a), None, 0, None) == L.OK
+    for code in (0, -1, -2, -3, -4, -5, -6, -7, -99):
+        assert len(L.strerror(code)) > 5
+    assert b"gfx950" in lib.moe_fp8_version()
+
+
+def test_no_device_is_reported(pkg, lib):
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    L = pkg._lib
+    a = _args(pkg)
+    assert lib.moe_fp8_run(ctypes.byref(a), 0x1000, L.workspace_bytes(4), None) == L.EDEVICE
