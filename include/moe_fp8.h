@@ -99,7 +99,7 @@ typedef struct moe_fp8_args {
  *   sorted_slot   int32 [N_max]     flat slot t*8+k of each assignment
  *   token_nlocal  int32 [T]         number of local assignments of each token
  *   work_items    int32 [max_items, 4]  GEMM work list (expert, first row, rows, 0)  (kernel.py:384-407)
- *   counters      int32 [16]        [0] number of work items, [1] N, [2] ticket counter
+ *   counters      int32 [16]        [0] number of work items, [1] N; the rest reserved
  *   act           fp8   [N_max, 2048]    SwiGLU output requantised to e4m3fn          (kernel.py:669)
  *   act_scale     fp32  [N_max, 16]      its 1x128 block scales, row-major per row   (kernel.py:670)
  *   partial       fp32  [T*8, 7168]      weighted GEMM2 rows of tokens with more than one local

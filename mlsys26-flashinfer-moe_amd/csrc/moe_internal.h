@@ -4,7 +4,9 @@
 //   caller tensors   : the contract of kernel.py:591-607 (see include/moe_fp8.h)
 //   workspace arrays : moe_fp8_layout offsets; every array is 256-byte aligned.
 // Kernels of one call run in this order on one stream:
-//   route_dispatch_kernel -> [place_kernel] -> gemm1_kernel -> gemm2_kernel -> combine_kernel
+//   route_dispatch_small_kernel | (route_count_kernel -> scan_kernel -> place_kernel)
+//   -> GEMM1 -> GEMM2 -> combine_kernel
+// where the GEMMs are gemm_stream_kernel (<= 32 rows per work item) or gemm_tile_kernel.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -29,14 +31,12 @@ constexpr int kIBlocks = MOE_FP8_I_BLOCKS;     // 16
 // Routing: one wavefront per token, 16 tokens per work-group of 1024 threads.
 constexpr int kRouteTokensPerBlock = 16;
 constexpr int kRouteThreads = 64 * kRouteTokensPerBlock;
-// Up to this many tokens the last routing work-group also places every assignment,
-// so dispatch needs no second launch.
+// Up to this many tokens routing and dispatch run in a single work-group (one launch).
 constexpr int kSinglePassTokens = 256;
 
 // Control block (workspace counters[]).
 constexpr int kCtrItems = 0;    // number of GEMM work items
 constexpr int kCtrAssign = 1;   // N, the number of local assignments
-constexpr int kCtrTicket = 2;   // routing work-groups finished (reset by the last one)
 constexpr int kNumCounters = 16;
 
 // GEMM tiling shared by host and device.
@@ -50,7 +50,7 @@ constexpr int kGemmWaves = 8;
 inline int rows_per_item_for(int T) {
   if (T <= 64) return 16;
   if (T <= 512) return 32;
-  return 32;
+  return 128;
 }
 
 int compute_layout(int32_t T, moe_fp8_layout* out);
@@ -110,5 +110,7 @@ hipError_t launch_route_dispatch(const RouteParams& p, hipStream_t s);
 hipError_t launch_gemm1(const GemmParams& p, int rows_per_item, hipStream_t s);
 hipError_t launch_gemm2(const GemmParams& p, int rows_per_item, hipStream_t s);
 hipError_t launch_combine(const GemmParams& p, hipStream_t s);
+hipError_t launch_gemm1_tile(const GemmParams& p, hipStream_t s);
+hipError_t launch_gemm2_tile(const GemmParams& p, hipStream_t s);
 
 }  // namespace moe

@@ -56,10 +56,21 @@ def tile_schedule(token_counts: np.ndarray, block_m: int):
 
 
 def work_items(expert_count: np.ndarray, expert_start: np.ndarray, rows_per_item: int) -> np.ndarray:
-    """[n, 3] int32 rows (expert, first sorted row, rows): each expert's bucket cut into
-    runs of rows_per_item rows, experts in ascending order."""
+    """[n, 4] int32 rows (expert, first sorted row, rows, first item of the expert |
+    items of the expert << 16): each expert's bucket cut into runs of at most
+    rows_per_item rows, experts in ascending order. Above 32 rows per item the runs are
+    balanced: the run length is ceil(n / ceil(n / rows_per_item)) rounded up to 16."""
     out = []
     for e, n in enumerate(np.asarray(expert_count)):
-        for c in range(0, int(n), rows_per_item):
-            out.append((e, int(expert_start[e]) + c, min(rows_per_item, int(n) - c)))
-    return np.asarray(out, dtype=np.int32).reshape(-1, 3)
+        n = int(n)
+        if n == 0:
+            continue
+        chunk = rows_per_item
+        if rows_per_item > 32:
+            nmax = -(-n // rows_per_item)
+            chunk = min(rows_per_item, ((-(-n // nmax)) + 15) // 16 * 16)
+        starts = list(range(0, n, chunk))
+        first = len(out)
+        for c in starts:
+            out.append((e, int(expert_start[e]) + c, min(chunk, n - c), first | (len(starts) << 16)))
+    return np.asarray(out, dtype=np.int32).reshape(-1, 4)

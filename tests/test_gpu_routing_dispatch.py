@@ -51,9 +51,14 @@ def _check_dispatch(ws, gh, ids, w, offset, T):
     rpi = int(ws.layout.rows_per_item)
     items = odsp.work_items(d["expert_count"], d["expert_start"], rpi)
     assert c[0] == len(items)
-    got = gh.read(ws, "work_items", torch.int32, 4 * len(items)).reshape(-1, 4)[:, :3]
+    got = gh.read(ws, "work_items", torch.int32, 4 * len(items)).reshape(-1, 4)
     assert np.array_equal(got, items)
-    assert c[2] == 0, "ticket counter must be reset for the next call"
+    # every bucket row is covered exactly once by the work list
+    cover = np.zeros(n, dtype=np.int32)
+    for e, r0, rows, _ in items:
+        assert d["expert_start"][e] <= r0 and r0 + rows <= d["expert_start"][e + 1] and 0 < rows <= rpi
+        cover[r0:r0 + rows] += 1
+    assert np.all(cover == 1)
 
 
 @pytest.mark.parametrize("part", [0, 1, 2])
@@ -115,11 +120,11 @@ def test_dispatch_matches_oracle(T, offset):
     _check_dispatch(ws, gh, rid, rw, offset, T)
 
 
+@pytest.mark.parametrize("T", [60, 300])
 @pytest.mark.parametrize("case", ["one_expert", "none_local", "all_local", "repeat"])
-def test_dispatch_given_topk(case):
+def test_dispatch_given_topk(case, T):
     gh = _gh()
     dev = torch.device("cuda:0")
-    T = 300
     rng = np.random.default_rng(4)
     ids = np.stack([rng.permutation(256)[:8] for _ in range(T)]).astype(np.int32)
     if case == "one_expert":
