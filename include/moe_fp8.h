@@ -104,6 +104,8 @@ typedef struct moe_fp8_args {
  *   act_scale     fp32  [N_max, 16]      its 1x128 block scales, row-major per row   (kernel.py:670)
  *   partial       fp32  [T*8, 7168]      weighted GEMM2 rows of tokens with more than one local
  *                                        assignment, indexed by flat slot             (kernel.py:704)
+ *   swiglu        fp32  [N_max, 2048]    SwiGLU output before requantisation; only for
+ *                                        T <= 512 (0 bytes otherwise)
  */
 typedef struct moe_fp8_layout {
   size_t total_bytes;
@@ -122,6 +124,7 @@ typedef struct moe_fp8_layout {
   size_t act;
   size_t act_scale;
   size_t partial;
+  size_t swiglu;
   int32_t num_tokens;
   int32_t max_assignments;   /* N_max = 8*T        */
   int32_t max_work_items;

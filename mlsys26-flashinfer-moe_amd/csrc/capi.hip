@@ -95,6 +95,7 @@ GemmParams gemm_params(const moe_fp8_args* a, const moe_fp8_layout& L, void* ws)
   p.act = at<uint8_t>(ws, L.act);
   p.act_scale = at<float>(ws, L.act_scale);
   p.partial = at<float>(ws, L.partial);
+  p.swiglu = at<float>(ws, L.swiglu);
   p.out = a->output;
   p.out_dtype = a->output_dtype;
   p.topk_ids = at<int32_t>(ws, L.topk_ids);
@@ -135,6 +136,7 @@ int compute_layout(int32_t T, moe_fp8_layout* out) {
   L.act = take(nmax * kInter);
   L.act_scale = take(nmax * kIBlocks * sizeof(float));
   L.partial = take(t * kTopK * kHidden * sizeof(float));
+  L.swiglu = take(rpi <= 32 ? nmax * kInter * sizeof(float) : 0);
   L.total_bytes = off;
   L.num_tokens = T;
   L.max_assignments = (int32_t)nmax;

@@ -1,33 +1,29 @@
-// Grouped fp8 block-scale GEMMs of the MoE layer on gfx950 MFMA.
+// Decode-regime grouped fp8 block-scale GEMMs (gfx950 MFMA), the requantisation pass and
+// the per-token combine of the MoE layer.
 //
-// Work item = (local expert e, a run of <= ROWS consecutive rows of e's bucket in the
-// sorted assignment order). A work-group of 8 wavefronts takes one work item and one
-// slice of output columns:
-//   GEMM1: 128 SwiGLU columns -> 128 gate rows + 128 up rows of W13[e]; 16 column slices.
-//   GEMM2: 256 hidden rows of W2[e]; 28 row slices.
-// Each wavefront owns 32 weight rows (two 16-row MFMA fragments) and streams them from
-// HBM straight into registers, several K-steps ahead. Every K-step is exactly one 128x128
-// scale block, so one v_mfma_f32_16x16x128_f8f6f4 per fragment pair is followed by
-// acc += mfma * (s_act[row,k] * s_w[block,k]) in fp32 (kernel.py:123-124 and :234).
-//
-// gemm_stream_kernel serves items of <= 32 rows (the decode regime): each wavefront also
-// loads the activation fragments of the item itself, into the same in-order register ring
-// as its weights; there is no LDS traffic and no barrier in the K loop. Items of up to 128
-// rows go to the tile kernels of gemm_tile.hip.
+// Work item = (local expert e, a run of <= 32 consecutive rows of e's bucket in the sorted
+// assignment order). In this regime the layer streams the weights of the touched experts
+// once from HBM, so the work is cut per WAVEFRONT, not per work-group: a work unit is
+// (item, weight slice of one wavefront), and the units are dealt round-robin over the
+// work-groups, so that every CU streams about the same number of bytes:
+//   GEMM1: slice = 16 SwiGLU columns = 16 gate rows + the matching 16 up rows of W13[e]
+//          (128 slices); the epilogue writes C = silu(X2) * X1 in fp32 (kernel.py:126-129),
+//          and requant_kernel turns each row's 128-column blocks into e4m3 with
+//          scale = max(amax/448, 1e-12) (kernel.py:131-135 uses 64-column blocks; this
+//          layer uses 128 so that GEMM2 sees one activation scale per K-step).
+//   GEMM2: slice = 32 hidden rows of W2[e] (224 slices); v = acc * routing weight
+//          (kernel.py:236-237); a token with one local assignment gets v written straight
+//          to its output row, the others park v in `partial` by flat slot for
+//          combine_kernel (the reference adds with fp32 atomics, kernel.py:246-250).
+// A wavefront streams its weight rows and the item's activation rows into a 4-deep
+// register ring (3 K-steps in flight). Every K-step is exactly one 128x128 scale block:
+// one v_mfma_f32_16x16x128_f8f6f4 per fragment pair, then acc += mfma * (s_act * s_w) in
+// fp32 (kernel.py:123-124 and :234).
 //
 // K-byte permutation: inside each 128-byte K block, lane group g = lane/16 holds bytes
 // [16g, 16g+16) and [64+16g, 64+16g+16) of its row (weights and activations alike, so the
 // dot products are unchanged). Each 16-byte load instruction of a wavefront then reads
 // whole 64-byte segments of 16 rows.
-//
-// Epilogues:
-//   GEMM1: C = silu(X2) * X1 with X1 the first I columns and X2 the second (kernel.py:126-129),
-//          then per row and 128 columns: scale = max(amax/448, 1e-12), q = e4m3(C/scale)
-//          (kernel.py:131-135 uses 64-column blocks; this layer uses 128 so that GEMM2 sees
-//          one activation scale per K-step).
-//   GEMM2: v = acc * routing weight (kernel.py:236-237); a token with one local assignment
-//          gets v written straight to its output row, others park v in `partial` by flat
-//          slot for combine_kernel (the reference adds with fp32 atomics, kernel.py:246-250).
 #include "moe_internal.h"
 #include "moe_device.h"
 
@@ -37,20 +33,21 @@ namespace {
 
 constexpr int kG1 = 1;
 constexpr int kG2 = 2;
+constexpr int kStreamWaves = 4;                      // wavefronts per work-group
+constexpr int kG1Slices = kInter / 16;               // 128 slices of 16 SwiGLU columns
+constexpr int kG2Slices = kHidden / 32;              // 224 slices of 32 hidden rows
 
 template <int KIND>
-struct GemmShape;
+struct StreamShape;
 template <>
-struct GemmShape<kG1> {
-  static constexpr int kSteps = kHBlocks;        // K = 7168
-  static constexpr int kRowBytes = kHidden;      // activation row stride
-  static constexpr int kSlices = kG1ColBlocks;   // 16
+struct StreamShape<kG1> {
+  static constexpr int kSteps = kHBlocks;   // K = 7168
+  static constexpr int kSlices = kG1Slices;
 };
 template <>
-struct GemmShape<kG2> {
-  static constexpr int kSteps = kIBlocks;        // K = 2048
-  static constexpr int kRowBytes = kInter;
-  static constexpr int kSlices = kG2RowBlocks;   // 28
+struct StreamShape<kG2> {
+  static constexpr int kSteps = kIBlocks;   // K = 2048
+  static constexpr int kSlices = kG2Slices;
 };
 
 // One MFMA operand fragment: bytes [16g, 16g+16) and [64+16g, +16) of a 128-byte K block
@@ -61,210 +58,183 @@ __device__ __forceinline__ v8i load_frag(const uint8_t* p) {
   return join(lo, hi);
 }
 
-// Decodes work index w into (item, slice): all slices of an item stay on one XCD (w % 8),
-// so the item's activation rows are fetched into one L2.
-template <int SLICES>
-__device__ __forceinline__ bool decode_work(int w, int n_items, int& item, int& slice) {
-  const int xcd = w & 7, loc = w >> 3;
-  slice = loc % SLICES;
-  item = (loc / SLICES) * 8 + xcd;
-  return item < n_items;
-}
+template <int NG>
+struct StreamStage {
+  v8i w[2];
+  v8i a[NG];
+  float sa[NG];
+};
 
-// Weight fragment rows and block-scale rows of this wavefront.
-template <int KIND>
-__device__ __forceinline__ void weight_rows(const GemmParams& p, int e, int slice, int wave, int lane,
-                                            const uint8_t*& wf0, const uint8_t*& wf1, const float*& sw0,
-                                            const float*& sw1) {
+// One work unit for an item of NG row groups (NG <= 2). Every K-step has the same shape:
+// loads past the last step repeat the last step (cache-hot) into ring slots that are never
+// read, and the weight block scales come from lane registers through readlane, so the loop
+// holds no branches and the compiler's waits cover exactly the step being consumed.
+template <int KIND, int NG>
+__device__ __forceinline__ void stream_unit(const GemmParams& p, int e, int r0, int rows, int slice, int lane) {
+  constexpr int KS = StreamShape<KIND>::kSteps;
+  constexpr int NB = 4;
+  static_assert(KS % NB == 0, "K-step count");
+
+  // weight fragments and their block-scale rows
+  const uint8_t* wf0;
+  const uint8_t* wf1;
+  const float* sw0;
+  const float* sw1;
   if constexpr (KIND == kG1) {
-    const int row = slice * kG1ColsPerBlock + wave * 16 + (lane & 15);   // gate row; up = +I
+    const int row = slice * 16 + (lane & 15);                 // gate row; up row = + I
     wf0 = p.w13 + ((size_t)e * 2 * kInter + row) * kHidden + (lane >> 4) * 16;
     wf1 = wf0 + (size_t)kInter * kHidden;
-    sw0 = p.w13_scale + ((size_t)e * 32 + slice) * kHBlocks;
-    sw1 = p.w13_scale + ((size_t)e * 32 + kIBlocks + slice) * kHBlocks;
+    sw0 = p.w13_scale + ((size_t)e * 32 + slice / 8) * kHBlocks;
+    sw1 = p.w13_scale + ((size_t)e * 32 + kIBlocks + slice / 8) * kHBlocks;
   } else {
-    const int row = slice * kG2RowsPerBlock + wave * 32 + (lane & 15);
+    const int row = slice * 32 + (lane & 15);                 // rows +0 and +16
     wf0 = p.w2 + ((size_t)e * kHidden + row) * kInter + (lane >> 4) * 16;
     wf1 = wf0 + (size_t)16 * kInter;
-    sw0 = p.w2_scale + ((size_t)e * kHBlocks + (slice * kG2RowsPerBlock + wave * 32) / 128) * kIBlocks;
+    sw0 = p.w2_scale + ((size_t)e * kHBlocks + slice / 4) * kIBlocks;
     sw1 = sw0;
   }
-}
+  const float sw0_lane = sw0[lane < KS ? lane : 0];
+  const float sw1_lane = sw1[lane < KS ? lane : 0];
 
-// GEMM1 epilogue: SwiGLU, row amax over the work-group's 128 columns, fp8 requantisation.
-template <int GROUPS>
-__device__ __forceinline__ void epilogue_gemm1(const GemmParams& p, const v4f (&acc0)[GROUPS],
-                                               const v4f (&acc1)[GROUPS], int ng, int rows, int r0,
-                                               int slice, int wave, int lane,
-                                               float (*s_amax)[GROUPS * 16]) {
-  float c[GROUPS][4];
+  // activation rows of this lane's column in each 16-row group (rows past the item's end
+  // read its first row; their results are never stored)
+  const uint8_t* ap[NG];
+  const float* sap[NG];
 #pragma unroll
-  for (int g = 0; g < GROUPS; ++g) {
-    if (g < ng) {
-      float amax = 0.f;
+  for (int g = 0; g < NG; ++g) {
+    const int m = g * 16 + (lane & 15);
+    const int mm = m < rows ? m : 0;
+    if constexpr (KIND == kG1) {
+      const int tok = p.sorted_token[r0 + mm];
+      ap[g] = p.hidden + (size_t)tok * kHidden + (lane >> 4) * 16;
+      sap[g] = p.hidden_scale + tok;
+    } else {
+      ap[g] = p.act + (size_t)(r0 + mm) * kInter + (lane >> 4) * 16;
+      sap[g] = p.act_scale + (size_t)(r0 + mm) * kIBlocks;
+    }
+  }
+  const size_t sa_stride = (KIND == kG1) ? (size_t)p.T : 1;
+
+  StreamStage<NG> ring[NB];
+  auto issue = [&](int k, StreamStage<NG>& st) {
+    st.w[0] = load_frag(wf0 + k * 128);
+    st.w[1] = load_frag(wf1 + k * 128);
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      st.a[g] = load_frag(ap[g] + k * 128);
+      st.sa[g] = sap[g][k * sa_stride];
+    }
+  };
+#pragma unroll
+  for (int s = 0; s < NB - 1; ++s) issue(s, ring[s]);
+
+  v4f acc0[NG], acc1[NG];
+#pragma unroll
+  for (int g = 0; g < NG; ++g) {
+    acc0[g] = v4f{0.f, 0.f, 0.f, 0.f};
+    acc1[g] = v4f{0.f, 0.f, 0.f, 0.f};
+  }
+  const v4f zero = {0.f, 0.f, 0.f, 0.f};
+#pragma nounroll
+  for (int k0 = 0; k0 < KS; k0 += NB) {
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+      const int k = k0 + u;
+      issue(min(k + NB - 1, KS - 1), ring[(u + NB - 1) % NB]);
+      // keep each step's loads ahead of its math (the scheduler would otherwise pull later
+      // steps' MFMAs above these loads and shrink the ring to one step in flight)
+      __builtin_amdgcn_sched_barrier(0);
+      const StreamStage<NG>& st = ring[u];
+      const float s0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sw0_lane), k));
+      const float s1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sw1_lane), k));
+#pragma unroll
+      for (int g = 0; g < NG; ++g) {
+        const v4f d0 = mfma16x16x128_fp8(st.w[0], st.a[g], zero);
+        const v4f d1 = mfma16x16x128_fp8(st.w[1], st.a[g], zero);
+        acc0[g] += d0 * (st.sa[g] * s0);
+        acc1[g] += d1 * (st.sa[g] * s1);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+
+  // lane: column (lane & 15) of each row group, fragment rows 4*(lane>>4) + i
+#pragma unroll
+  for (int g = 0; g < NG; ++g) {
+    const int m = g * 16 + (lane & 15);
+    if (m >= rows) continue;
+    const int pr = r0 + m;
+    if constexpr (KIND == kG1) {
+      v4f c;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const float x1 = acc0[g][i], x2 = acc1[g][i];
-        c[g][i] = (x2 / (1.0f + __expf(-x2))) * x1;
-        amax = fmaxf(amax, fabsf(c[g][i]));
+        c[i] = (x2 / (1.0f + __expf(-x2))) * x1;
       }
-      amax = fmaxf(amax, __shfl_xor(amax, 16));
-      amax = fmaxf(amax, __shfl_xor(amax, 32));
-      if (lane < 16) s_amax[wave][g * 16 + lane] = amax;
-    }
-  }
-  __syncthreads();
+      *reinterpret_cast<v4f*>(p.swiglu + (size_t)pr * kInter + slice * 16 + 4 * (lane >> 4)) = c;
+    } else {
+      const int t = p.sorted_token[pr];
+      const float wt = p.sorted_weight[pr];
+      const bool direct = p.token_nlocal[t] == 1;
+      const size_t slot = (size_t)p.sorted_slot[pr];
 #pragma unroll
-  for (int g = 0; g < GROUPS; ++g) {
-    if (g < ng) {
-      const int m = g * 16 + (lane & 15);
-      float amax = s_amax[0][m];
-#pragma unroll
-      for (int ww = 1; ww < kGemmWaves; ++ww) amax = fmaxf(amax, s_amax[ww][m]);
-      const float scale = fmaxf(amax / 448.0f, 1e-12f);
-      if (m < rows) {
-        const uint32_t q = pack_fp8x4(c[g][0] / scale, c[g][1] / scale, c[g][2] / scale, c[g][3] / scale);
-        const int col = slice * kG1ColsPerBlock + wave * 16 + 4 * (lane >> 4);
-        *reinterpret_cast<uint32_t*>(p.act + (size_t)(r0 + m) * kInter + col) = q;
-        if (wave == 0 && lane < 16) p.act_scale[(size_t)(r0 + m) * kIBlocks + slice] = scale;
-      }
-    }
-  }
-  __syncthreads();
-}
-
-// GEMM2 epilogue: weight by the routing weight; single-assignment tokens write their output
-// row directly, the others park the row in `partial` under its flat slot.
-template <int GROUPS>
-__device__ __forceinline__ void epilogue_gemm2(const GemmParams& p, const v4f (&acc0)[GROUPS],
-                                               const v4f (&acc1)[GROUPS], int ng, int rows, int r0,
-                                               int slice, int wave, int lane) {
-#pragma unroll
-  for (int g = 0; g < GROUPS; ++g) {
-    if (g < ng) {
-      const int m = g * 16 + (lane & 15);
-      if (m < rows) {
-        const int pr = r0 + m;
-        const int t = p.sorted_token[pr];
-        const float wt = p.sorted_weight[pr];
-        const bool direct = p.token_nlocal[t] == 1;
-        const size_t slot = (size_t)p.sorted_slot[pr];
-#pragma unroll
-        for (int f = 0; f < 2; ++f) {
-          const v4f v = (f == 0 ? acc0[g] : acc1[g]) * wt;
-          const int h = slice * kG2RowsPerBlock + wave * 32 + f * 16 + 4 * (lane >> 4);
-          if (direct) {
-            if (p.out_dtype == MOE_FP8_OUT_BF16) {
-              *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(p.out) + (size_t)t * kHidden + h) =
-                  pack_bf16x4(v[0], v[1], v[2], v[3]);
-            } else {
-              *reinterpret_cast<v4f*>(reinterpret_cast<float*>(p.out) + (size_t)t * kHidden + h) = v;
-            }
-          } else {
-            *reinterpret_cast<v4f*>(p.partial + slot * kHidden + h) = v;
-          }
+      for (int f = 0; f < 2; ++f) {
+        const v4f v = (f == 0 ? acc0[g] : acc1[g]) * wt;
+        const int h = slice * 32 + f * 16 + 4 * (lane >> 4);
+        if (direct) {
+          if (p.out_dtype == MOE_FP8_OUT_BF16)
+            *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(p.out) + (size_t)t * kHidden + h) =
+                pack_bf16x4(v[0], v[1], v[2], v[3]);
+          else
+            *reinterpret_cast<v4f*>(reinterpret_cast<float*>(p.out) + (size_t)t * kHidden + h) = v;
+        } else {
+          *reinterpret_cast<v4f*>(p.partial + slot * kHidden + h) = v;
         }
       }
     }
   }
 }
 
-template <int GROUPS>
-struct StreamStage {
-  v8i w[2];
-  v8i a[GROUPS];
-  float sa[GROUPS];
-  float sw[2];
-};
-
-template <int KIND, int GROUPS, int NB>
-__global__ __launch_bounds__(512) void gemm_stream_kernel(GemmParams p) {
-  using S = GemmShape<KIND>;
-  constexpr int KS = S::kSteps;
-  __shared__ float s_amax[kGemmWaves][GROUPS * 16];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
+template <int KIND, int MAXNG>
+__global__ __launch_bounds__(kStreamWaves * 64) void gemm_stream_kernel(GemmParams p) {
+  constexpr int SL = StreamShape<KIND>::kSlices;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n_items = min(p.counters[kCtrItems], p.max_items);
-  const int n_work = ((n_items + 7) & ~7) * S::kSlices;
-
-  for (int w = blockIdx.x; w < n_work; w += gridDim.x) {
-    int item, slice;
-    if (!decode_work<S::kSlices>(w, n_items, item, slice)) continue;
+  const int units = n_items * SL;
+  const int nwaves = gridDim.x * kStreamWaves;
+  // unit u runs on wavefront (u % gridDim.x, (u / gridDim.x) % kStreamWaves): consecutive
+  // units land on different work-groups, i.e. different CUs
+  for (int u = wave * gridDim.x + blockIdx.x; u < units; u += nwaves) {
+    const int item = u / SL, slice = u - (u / SL) * SL;
     const int4 it = reinterpret_cast<const int4*>(p.work_items)[item];
-    const int e = it.x, r0 = it.y, rows = it.z;
-    const int ng = (rows + 15) >> 4;
+    const int e = __builtin_amdgcn_readfirstlane(it.x);
+    const int r0 = __builtin_amdgcn_readfirstlane(it.y);
+    const int rows = __builtin_amdgcn_readfirstlane(it.z);
+    if (MAXNG == 1 || rows <= 16) stream_unit<KIND, 1>(p, e, r0, rows, slice, lane);
+    else stream_unit<KIND, MAXNG>(p, e, r0, rows, slice, lane);
+  }
+}
 
-    const uint8_t *wf0, *wf1;
-    const float *sw0, *sw1;
-    weight_rows<KIND>(p, e, slice, wave, lane, wf0, wf1, sw0, sw1);
-
-    // Activation rows of this lane's column in each 16-row group (rows past the item's end
-    // read its first row; their results are never stored).
-    const uint8_t* ap[GROUPS];
-    const float* sap[GROUPS];
+// Requantises the fp32 SwiGLU rows: per row and 128 columns, scale = max(amax/448, 1e-12)
+// and q = e4m3(c / scale) (kernel.py:131-135 with 128-column blocks). One work-group of 256
+// threads per row; 16 threads (8 columns each) per block.
+__global__ __launch_bounds__(256) void requant_kernel(GemmParams p) {
+  const int n = p.counters[kCtrAssign];
+  const int tid = threadIdx.x;
+  for (int r = blockIdx.x; r < n; r += gridDim.x) {
+    const v4f* src = reinterpret_cast<const v4f*>(p.swiglu + (size_t)r * kInter) + 2 * tid;
+    const v4f a = src[0], b = src[1];
+    float amax = fmaxf(fmaxf(fmaxf(fabsf(a[0]), fabsf(a[1])), fmaxf(fabsf(a[2]), fabsf(a[3]))),
+                       fmaxf(fmaxf(fabsf(b[0]), fabsf(b[1])), fmaxf(fabsf(b[2]), fabsf(b[3]))));
 #pragma unroll
-    for (int g = 0; g < GROUPS; ++g) {
-      const int m = g * 16 + (lane & 15);
-      const int mm = m < rows ? m : 0;
-      if constexpr (KIND == kG1) {
-        const int tok = p.sorted_token[r0 + mm];
-        ap[g] = p.hidden + (size_t)tok * kHidden + (lane >> 4) * 16;
-        sap[g] = p.hidden_scale + tok;
-      } else {
-        ap[g] = p.act + (size_t)(r0 + mm) * kInter + (lane >> 4) * 16;
-        sap[g] = p.act_scale + (size_t)(r0 + mm) * kIBlocks;
-      }
-    }
-    const size_t sa_stride = (KIND == kG1) ? (size_t)p.T : 1;
-
-    StreamStage<GROUPS> ring[NB];
-    auto issue = [&](int k, StreamStage<GROUPS>& st) {
-      st.w[0] = load_frag(wf0 + k * 128);
-      st.w[1] = load_frag(wf1 + k * 128);
-#pragma unroll
-      for (int g = 0; g < GROUPS; ++g) {
-        if (g < ng) {
-          st.a[g] = load_frag(ap[g] + k * 128);
-          st.sa[g] = sap[g][k * sa_stride];
-        }
-      }
-      st.sw[0] = sw0[k];
-      st.sw[1] = sw1[k];
-    };
-#pragma unroll
-    for (int s = 0; s < NB - 1; ++s)
-      if (s < KS) issue(s, ring[s]);
-
-    v4f acc0[GROUPS], acc1[GROUPS];
-#pragma unroll
-    for (int g = 0; g < GROUPS; ++g) {
-      acc0[g] = v4f{0.f, 0.f, 0.f, 0.f};
-      acc1[g] = v4f{0.f, 0.f, 0.f, 0.f};
-    }
-    const v4f zero = {0.f, 0.f, 0.f, 0.f};
-    for (int k0 = 0; k0 < KS; k0 += NB) {
-#pragma unroll
-      for (int u = 0; u < NB; ++u) {
-        const int k = k0 + u;
-        if (k < KS) {
-          if (k + NB - 1 < KS) issue(k + NB - 1, ring[(u + NB - 1) % NB]);
-          const StreamStage<GROUPS>& st = ring[u];
-#pragma unroll
-          for (int g = 0; g < GROUPS; ++g) {
-            if (g < ng) {
-              const v4f d0 = mfma16x16x128_fp8(st.w[0], st.a[g], zero);
-              const v4f d1 = mfma16x16x128_fp8(st.w[1], st.a[g], zero);
-              acc0[g] += d0 * (st.sa[g] * st.sw[0]);
-              acc1[g] += d1 * (st.sa[g] * st.sw[1]);
-            }
-          }
-        }
-      }
-    }
-    if constexpr (KIND == kG1) epilogue_gemm1<GROUPS>(p, acc0, acc1, ng, rows, r0, slice, wave, lane, s_amax);
-    else epilogue_gemm2<GROUPS>(p, acc0, acc1, ng, rows, r0, slice, wave, lane);
+    for (int off = 1; off < 16; off <<= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+    const float scale = fmaxf(amax / 448.0f, 1e-12f);
+    uint2 q;
+    q.x = pack_fp8x4(a[0] / scale, a[1] / scale, a[2] / scale, a[3] / scale);
+    q.y = pack_fp8x4(b[0] / scale, b[1] / scale, b[2] / scale, b[3] / scale);
+    reinterpret_cast<uint2*>(p.act + (size_t)r * kInter)[tid] = q;
+    if ((tid & 15) == 0) p.act_scale[(size_t)r * kIBlocks + (tid >> 4)] = scale;
   }
 }
 
@@ -304,43 +274,53 @@ int num_cus() {
   return cached[dev];
 }
 
-int persistent_grid(int max_work, int blocks_per_cu) {
-  int grid = num_cus() * blocks_per_cu;
-  grid = (grid + 7) & ~7;
-  return grid < max_work ? grid : max_work;
+// Work-groups of `kernel` that one CU holds at once (cached per kernel; 1 if unknown).
+template <typename K>
+int resident_per_cu(K kernel, int& cache) {
+  if (!cache) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, kStreamWaves * 64, 0) != hipSuccess || n <= 0) n = 1;
+    cache = n;
+  }
+  return cache;
+}
+
+// One wave of resident work-groups: every work-group starts at once, and the round-robin
+// deal gives every CU the same number of units (a second, partial wave of work-groups
+// would run at a fraction of the occupancy).
+template <int KIND, int MAXNG>
+hipError_t launch_stream_ng(const GemmParams& p, hipStream_t s) {
+  static int occ = 0;
+  const auto kernel = gemm_stream_kernel<KIND, MAXNG>;
+  const int max_units = p.max_items * StreamShape<KIND>::kSlices;
+  int grid = num_cus() * resident_per_cu(kernel, occ);
+  const int cap = (max_units + kStreamWaves - 1) / kStreamWaves;
+  if (grid > cap) grid = cap;
+  if (grid <= 0) return hipSuccess;
+  hipLaunchKernelGGL(kernel, dim3(grid), dim3(kStreamWaves * 64), 0, s, p);
+  return hipGetLastError();
 }
 
 template <int KIND>
-hipError_t launch_rows(const GemmParams& p, int rows_per_item, hipStream_t s) {
-  using S = GemmShape<KIND>;
-  const int max_work = ((p.max_items + 7) & ~7) * S::kSlices;
-  switch (rows_per_item) {
-    case 16: {
-      const int grid = persistent_grid(max_work, 2);
-      if (grid > 0) hipLaunchKernelGGL((gemm_stream_kernel<KIND, 1, 3>), dim3(grid), dim3(512), 0, s, p);
-      break;
-    }
-    case 32: {
-      const int grid = persistent_grid(max_work, 1);
-      if (grid > 0) hipLaunchKernelGGL((gemm_stream_kernel<KIND, 2, 3>), dim3(grid), dim3(512), 0, s, p);
-      break;
-    }
-    case 128:
-      return KIND == kG1 ? launch_gemm1_tile(p, s) : launch_gemm2_tile(p, s);
-    default:
-      return hipErrorInvalidValue;
-  }
-  return hipGetLastError();
+hipError_t launch_stream(const GemmParams& p, int rows_per_item, hipStream_t s) {
+  return rows_per_item <= 16 ? launch_stream_ng<KIND, 1>(p, s) : launch_stream_ng<KIND, 2>(p, s);
 }
 
 }  // namespace
 
 hipError_t launch_gemm1(const GemmParams& p, int rows_per_item, hipStream_t s) {
-  return launch_rows<kG1>(p, rows_per_item, s);
+  if (rows_per_item > 32) return launch_gemm1_tile(p, s);
+  const hipError_t e = launch_stream<kG1>(p, rows_per_item, s);
+  if (e != hipSuccess) return e;
+  int grid = p.max_items * rows_per_item;   // >= the number of SwiGLU rows
+  if (grid > num_cus() * 8) grid = num_cus() * 8;
+  if (grid > 0) hipLaunchKernelGGL(requant_kernel, dim3(grid), dim3(256), 0, s, p);
+  return hipGetLastError();
 }
 
 hipError_t launch_gemm2(const GemmParams& p, int rows_per_item, hipStream_t s) {
-  return launch_rows<kG2>(p, rows_per_item, s);
+  if (rows_per_item > 32) return launch_gemm2_tile(p, s);
+  return launch_stream<kG2>(p, rows_per_item, s);
 }
 
 hipError_t launch_combine(const GemmParams& p, hipStream_t s) {

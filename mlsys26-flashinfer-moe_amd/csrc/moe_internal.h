@@ -6,7 +6,8 @@
 // Kernels of one call run in this order on one stream:
 //   route_dispatch_small_kernel | (route_count_kernel -> scan_kernel -> place_kernel)
 //   -> GEMM1 -> GEMM2 -> combine_kernel
-// where the GEMMs are gemm_stream_kernel (<= 32 rows per work item) or gemm_tile_kernel.
+// where, with <= 32 rows per work item, GEMM1 is gemm_stream_kernel<1> + requant_kernel and
+// GEMM2 is gemm_stream_kernel<2>; with more rows both are gemm_tile_kernel.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -38,13 +39,6 @@ constexpr int kSinglePassTokens = 256;
 constexpr int kCtrItems = 0;    // number of GEMM work items
 constexpr int kCtrAssign = 1;   // N, the number of local assignments
 constexpr int kNumCounters = 16;
-
-// GEMM tiling shared by host and device.
-constexpr int kG1ColsPerBlock = 128;                 // SwiGLU output columns per GEMM1 work-group
-constexpr int kG1ColBlocks = kInter / kG1ColsPerBlock;   // 16
-constexpr int kG2RowsPerBlock = 256;                 // output (hidden) rows per GEMM2 work-group
-constexpr int kG2RowBlocks = kHidden / kG2RowsPerBlock;  // 28
-constexpr int kGemmWaves = 8;
 
 // Rows (assignments) per GEMM work item for a call with T tokens.
 inline int rows_per_item_for(int T) {
@@ -100,6 +94,7 @@ struct GemmParams {
   uint8_t* act;                // [N_max, 2048]
   float* act_scale;            // [N_max, 16]
   float* partial;              // [T*8, 7168]
+  float* swiglu;               // [N_max, 2048] (decode path)
   void* out;                   // [T, 7168]
   int out_dtype;
   const int32_t* topk_ids;

@@ -1,11 +1,13 @@
 // Routing and dispatch for the fused MoE layer (gfx950).
 //
-// One wavefront per token computes the DeepSeek-V3 no-aux grouped routing (kernel.py:428-542)
-// with DPP/readlane reductions. Dispatch then histograms the local assignments, scans them
-// into CSR offsets, builds the GEMM work list and places every assignment in its bucket:
-//   T <= 256: route_dispatch_small_kernel does everything in one work-group, in LDS;
-//   larger T: route_count_kernel (per work-group histograms and ranks) -> scan_kernel ->
-//             place_kernel. No kernel synchronises across work-groups.
+// Sixteen lanes per token (four tokens per wavefront) compute the DeepSeek-V3 no-aux grouped
+// routing (kernel.py:428-542) with branch-free DPP reductions inside 16-lane rows. Dispatch
+// then histograms the local assignments, scans them into CSR offsets, builds the GEMM work
+// list and places every assignment in its bucket:
+//   T <= 256: route_kernel<false> (16 tokens per work-group) -> dispatch_small_kernel, which
+//             does the whole dispatch in one work-group, in LDS;
+//   larger T: route_kernel<true> (also per work-group histograms and ranks) -> scan_kernel
+//             -> place_kernel. No kernel synchronises across work-groups.
 //
 // The order inside an expert's bucket is ascending token (then slot), i.e. a stable sort
 // by expert of the flat top-k list; the reference's atomic scatter (kernel.py:288-324)
@@ -50,115 +52,130 @@ __device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
   return ((uint64_t)hi << 32) | lo;
 }
 
-__device__ __forceinline__ uint64_t readlane_u64(uint64_t v, int l) {
-  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, l);
-  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), l);
-  return ((uint64_t)hi << 32) | lo;
-}
-
-// Argmax key of the routing: a larger fp32 value wins, then the lower index (the "lowest
-// index on ties" rule of kernel.py:499 and :525). The value is mapped to an unsigned key
-// that orders like the float (after -0 -> +0, so that equal values tie).
-__device__ __forceinline__ uint64_t argmax_key(float v, int idx) {
-  uint32_t u = __float_as_uint(v + 0.0f);
-  u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-  return ((uint64_t)u << 32) | (uint32_t)(0xFFFF - idx);
-}
-
+// Argmax keys of the routing: a larger fp32 value wins, then the lower expert index (the
+// "lowest index on ties" rule of kernel.py:499 and :525): key = ordered(v) << 32 | 0xFFFF - e.
 __device__ __forceinline__ int key_index(uint64_t key) { return 0xFFFF - (int)(key & 0xFFFFu); }
 
 __device__ __forceinline__ uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
 
-// Wave-wide maximum of a key, returned uniformly: DPP inside each 16-lane row, then the
-// four row results combined through readlane.
-__device__ __forceinline__ uint64_t wave_max_key(uint64_t k) {
-  k = max_u64(k, dpp_u64<kDppXor1>(k));
-  k = max_u64(k, dpp_u64<kDppXor2>(k));
-  k = max_u64(k, dpp_u64<kDppHalfMirror>(k));
-  k = max_u64(k, dpp_u64<kDppMirror>(k));
-  const uint64_t r0 = readlane_u64(k, 0), r1 = readlane_u64(k, 16);
-  const uint64_t r2 = readlane_u64(k, 32), r3 = readlane_u64(k, 48);
-  return max_u64(max_u64(r0, r1), max_u64(r2, r3));
+// Order-preserving map of a float to an unsigned key (after -0 -> +0, so equal values tie):
+// a > b as floats <=> ordered(a) > ordered(b).
+__device__ __forceinline__ uint32_t ordered(float v) {
+  const uint32_t u = __float_as_uint(v + 0.0f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+constexpr uint32_t kOrderedNegInf = 0x007FFFFFu;   // ordered(-inf)
+
+template <int CTRL>
+__device__ __forceinline__ int dpp_i32(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
 }
 
-// Routes token t with the calling wavefront. Lane l owns global experts 4l..4l+3.
-// On return every lane holds the 8 selected expert ids and weights in selection order.
-__device__ void route_token(const RouteParams& p, const float* s_bias, int t, int (&ids)[kTopK],
-                            float (&wts)[kTopK]) {
+// 1 if group pg with score pv ranks before group g with score gs in the group selection
+// (larger score first, lower index on ties); pv, pg come from the lane ROT lanes away
+// within the 16-lane row.
+template <int ROT>
+__device__ __forceinline__ int group_beats(float gs, int g) {
+  constexpr int kCtrl = 0x120 + ROT;   // DPP row_ror:ROT
+  const float pv = __int_as_float(dpp_i32<kCtrl>(__float_as_int(gs)));
+  const int pg = dpp_i32<kCtrl>(g);
+  return (pv > gs || (pv == gs && pg < g)) ? 1 : 0;
+}
+
+// Routing of 4 tokens by one wavefront (kernel.py:428-542). Token q = lane/16 of the
+// wavefront is t0 + q; lane r = lane%16 of its row holds experts 16r..16r+15, so group g
+// (32 experts) is lanes 2g, 2g+1. Returns in lanes r < 8 the expert of top-k slot r (in
+// selection order) and its weight; other lanes return id -1.
+__device__ __forceinline__ int route_wave(const RouteParams& p, const float* s_bias, int t0, float& w_out) {
   const int lane = lane_id();
-  const float4 lg = reinterpret_cast<const float4*>(p.logits + (size_t)t * kExpertsGlobal)[lane];
-  const float4 bs = reinterpret_cast<const float4*>(s_bias)[lane];
-  const float lgv[4] = {lg.x, lg.y, lg.z, lg.w};
-  const float bv[4] = {bs.x, bs.y, bs.z, bs.w};
-  float s[4], b[4];
+  const int r = lane & 15;
+  const int t = min(t0 + (lane >> 4), p.T - 1);   // rows past the end recompute the last token
+  const float4* lp = reinterpret_cast<const float4*>(p.logits + (size_t)t * kExpertsGlobal + 16 * r);
+  const float4* bp = reinterpret_cast<const float4*>(s_bias + 16 * r);
+  float s[16], b[16];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    s[i] = sigmoid_f32(lgv[i]);   // kernel.py:466
-    b[i] = s[i] + bv[i];          // kernel.py:467
+    const float4 x = lp[i], c = bp[i];
+    const float xs[4] = {x.x, x.y, x.z, x.w}, cs[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      s[4 * i + j] = sigmoid_f32(xs[j]);        // kernel.py:466
+      b[4 * i + j] = s[4 * i + j] + cs[j];      // kernel.py:467
+    }
   }
-  // Group score = sum of the two largest biased scores of the group (kernel.py:479-488).
-  // The 32 experts of group g live in lanes 8g..8g+7.
+  // Group score = sum of the two largest biased scores of the group (kernel.py:479-488):
+  // top-2 of the lane's 16 (median-of-three keeps the runner-up), then of the lane pair.
   float m1 = fmaxf(b[0], b[1]), m2 = fminf(b[0], b[1]);
-  top2_merge(m1, m2, fmaxf(b[2], b[3]), fminf(b[2], b[3]));
-  top2_merge(m1, m2, dpp_f32<kDppXor1>(m1), dpp_f32<kDppXor1>(m2));
-  top2_merge(m1, m2, dpp_f32<kDppXor2>(m1), dpp_f32<kDppXor2>(m2));
-  top2_merge(m1, m2, dpp_f32<kDppHalfMirror>(m1), dpp_f32<kDppHalfMirror>(m2));
-  const float my_group_score = m1 + m2;
-  float gs[kNGroup];
 #pragma unroll
-  for (int g = 0; g < kNGroup; ++g)
-    gs[g] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_group_score), g * 8));
-
-  // Keep the top-4 groups: 4 rounds of max over the unselected groups, lowest index on
-  // ties (kernel.py:495-501).
-  int selected = 0;
-#pragma unroll
-  for (int r = 0; r < kTopKGroup; ++r) {
-    float best = -INFINITY;
-#pragma unroll
-    for (int g = 0; g < kNGroup; ++g) {
-      const float v = ((selected >> g) & 1) ? -INFINITY : gs[g];
-      best = fmaxf(best, v);
-    }
-    int bg = kNGroup;
-#pragma unroll
-    for (int g = kNGroup - 1; g >= 0; --g) {
-      const float v = ((selected >> g) & 1) ? -INFINITY : gs[g];
-      if (!((selected >> g) & 1) && v == best) bg = g;
-    }
-    if (bg < kNGroup) selected |= 1 << bg;
+  for (int i = 2; i < 16; ++i) {
+    const float n2 = __builtin_amdgcn_fmed3f(m1, m2, b[i]);
+    m1 = fmaxf(m1, b[i]);
+    m2 = n2;
   }
+  top2_merge(m1, m2, dpp_f32<kDppXor1>(m1), dpp_f32<kDppXor1>(m2));
+  const float gs = m1 + m2;
+  // Keep the 4 best groups (kernel.py:495-501): a group is kept iff fewer than 4 groups
+  // rank before it. The seven other groups of the row are 2, 4, ..., 14 lanes away.
+  const int g = r >> 1;
+  const int rank = group_beats<2>(gs, g) + group_beats<4>(gs, g) + group_beats<6>(gs, g) +
+                   group_beats<8>(gs, g) + group_beats<10>(gs, g) + group_beats<12>(gs, g) +
+                   group_beats<14>(gs, g);
+  const bool kept = rank < kTopKGroup;
 
-  // Top-8 experts of the kept groups by biased score, lowest index on ties; the weight
-  // uses the unbiased score (kernel.py:515-534).
-  const bool mine = (selected >> (lane >> 3)) & 1;
-  float v[4];
+  // Top-8 experts of the kept groups by biased score, lowest index on ties (kernel.py:515-534):
+  // 8 rounds of (argmax inside the lane, argmax across the row on 64-bit keys
+  // (score key << 32 | 0xFFFF - expert), removal of the winner from its lane).
+  uint32_t c[16];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) v[i] = mine ? b[i] : -INFINITY;
+  for (int i = 0; i < 16; ++i) c[i] = kept ? ordered(b[i]) : kOrderedNegInf;
+  const uint32_t lo_base = 0xFFFFu - 16u * (uint32_t)r;
+  int my_id = -1;
 #pragma unroll
   for (int k = 0; k < kTopK; ++k) {
-    uint64_t best = argmax_key(v[0], 4 * lane);
+    uint32_t v8[8], i8[8], v4[4], i4[4], v2[2], i2[2];
 #pragma unroll
-    for (int i = 1; i < 4; ++i) best = max_u64(best, argmax_key(v[i], 4 * lane + i));
-    const int bi = key_index(wave_max_key(best));
-    const int owner = bi >> 2, sub = bi & 3;
-    const float my_s = sub == 0 ? s[0] : sub == 1 ? s[1] : sub == 2 ? s[2] : s[3];
-    wts[k] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_s), owner));
-    ids[k] = bi;
-    if (lane == owner) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        if (i == sub) v[i] = -INFINITY;
+    for (int j = 0; j < 8; ++j) {
+      const bool hi = c[2 * j + 1] > c[2 * j];
+      v8[j] = hi ? c[2 * j + 1] : c[2 * j];
+      i8[j] = hi ? 2 * j + 1 : 2 * j;
     }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const bool hi = v8[2 * j + 1] > v8[2 * j];
+      v4[j] = hi ? v8[2 * j + 1] : v8[2 * j];
+      i4[j] = hi ? i8[2 * j + 1] : i8[2 * j];
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const bool hi = v4[2 * j + 1] > v4[2 * j];
+      v2[j] = hi ? v4[2 * j + 1] : v4[2 * j];
+      i2[j] = hi ? i4[2 * j + 1] : i4[2 * j];
+    }
+    const bool hi = v2[1] > v2[0];
+    const uint32_t bv = hi ? v2[1] : v2[0];
+    const uint32_t bi = hi ? i2[1] : i2[0];
+    uint64_t key = ((uint64_t)bv << 32) | (lo_base - bi);
+    key = max_u64(key, dpp_u64<kDppXor1>(key));
+    key = max_u64(key, dpp_u64<kDppXor2>(key));
+    key = max_u64(key, dpp_u64<kDppHalfMirror>(key));
+    key = max_u64(key, dpp_u64<kDppMirror>(key));
+    const int e = key_index(key);
+    my_id = (r == k) ? e : my_id;
+    const uint32_t drop = ((e >> 4) == r) ? (uint32_t)(e & 15) : 16u;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) c[i] = (drop == (uint32_t)i) ? 0u : c[i];
   }
-  // Renormalise and scale: w = s / (sum s + 1e-20) * rsf, sum taken in selection order
-  // (kernel.py:537-538).
-  float sum = wts[0];
+  // Weights from the unbiased scores, renormalised in selection order and scaled
+  // (kernel.py:537-538): w = s / (s_0 + ... + s_7 + 1e-20) * rsf. Lane r < 8 recomputes
+  // the score of its expert; every lane then sums the row's eight in order.
+  const float sv = (r < kTopK) ? sigmoid_f32(p.logits[(size_t)t * kExpertsGlobal + my_id]) : 0.0f;
+  const int row0 = lane & 48;
+  float sum = __shfl(sv, row0);
 #pragma unroll
-  for (int k = 1; k < kTopK; ++k) sum = sum + wts[k];
+  for (int k = 1; k < kTopK; ++k) sum = sum + __shfl(sv, row0 | k);
   sum = sum + 1e-20f;
-#pragma unroll
-  for (int k = 0; k < kTopK; ++k) wts[k] = __fdiv_rn(wts[k], sum) * p.rsf;
+  w_out = __fdiv_rn(sv, sum) * p.rsf;
+  return r < kTopK ? my_id : -1;
 }
 
 __device__ __forceinline__ int local_of(int id, int offset) {
@@ -170,35 +187,6 @@ __device__ __forceinline__ int local_of(int id, int offset) {
 __device__ __forceinline__ void stage_bias(const RouteParams& p, float* s_bias) {
   if (!p.skip_routing && threadIdx.x < kExpertsGlobal) s_bias[threadIdx.x] = load_bias(p.bias, p.bias_dtype, threadIdx.x);
   __syncthreads();
-}
-
-// Routes token t with the calling wavefront (or reads its given top-k list) and stores the
-// result; returns, in lanes 0..7, the local expert index of slot t*8+lane (-1 if not local)
-// and its routing weight.
-__device__ __forceinline__ int route_or_load(const RouteParams& p, const float* s_bias, int t, float& w_out) {
-  const int lane = lane_id();
-  int id = -1;
-  float w = 0.f;
-  if (!p.skip_routing) {
-    int ids[kTopK];
-    float wts[kTopK];
-    route_token(p, s_bias, t, ids, wts);
-#pragma unroll
-    for (int k = 0; k < kTopK; ++k)
-      if (lane == k) { id = ids[k]; w = wts[k]; }
-    if (lane < kTopK) {
-      p.topk_ids[t * kTopK + lane] = id;
-      p.topk_w[t * kTopK + lane] = w;
-    }
-  } else if (lane < kTopK) {
-    id = p.topk_ids[t * kTopK + lane];
-    w = p.topk_w[t * kTopK + lane];
-  }
-  const int le = lane < kTopK ? local_of(id, p.offset) : -1;
-  const uint64_t local_mask = __ballot(le >= 0);
-  if (lane == 0) p.token_nlocal[t] = __popcll(local_mask);
-  w_out = w;
-  return le;
 }
 
 // Stable rank of each thread's slot among the work-group's slots with the same local expert
@@ -275,12 +263,55 @@ __device__ __forceinline__ void finish_counts(const RouteParams& p, int e, int r
 
 }  // namespace
 
-// Small batches (T <= kSinglePassTokens): routing and the whole dispatch in one work-group.
-// Each wavefront routes tokens wave, wave+16, ...; the local expert ids and weights of all
-// T*8 slots stay in LDS, are ranked 1024 at a time and placed without leaving the
-// work-group, so no cross-work-group synchronisation is needed.
-__global__ __launch_bounds__(kRouteThreads) void route_dispatch_small_kernel(RouteParams p) {
+// Routing (or, on given top-k lists, loading) of 16 tokens per work-group of 4 wavefronts.
+// With RANKS the work-group also records every token's local count, the stable rank of
+// each local slot among its 128 slots and its expert histogram (dispatch of large batches).
+constexpr int kRouteWaves = kRouteTokensPerBlock / 4;
+
+template <bool RANKS>
+__global__ __launch_bounds__(kRouteWaves * 64) void route_kernel(RouteParams p) {
   __shared__ __attribute__((aligned(16))) float s_bias[kExpertsGlobal];
+  __shared__ int s_le[kRouteTokensPerBlock * kTopK];
+  __shared__ int s_wcnt[16][kExpertsLocal];
+  __shared__ int s_cnt[kExpertsLocal];
+  const int tid = threadIdx.x;
+  const int lane = lane_id();
+  const int wave = tid >> 6;
+  const int r = lane & 15;
+  const int tw = blockIdx.x * kRouteTokensPerBlock + wave * 4;   // first token of the wavefront
+  const int t = tw + (lane >> 4);                                 // token of this lane's row
+  const bool slot_lane = t < p.T && r < kTopK;                    // lane holds slot t*8 + r
+  stage_bias(p, s_bias);
+  int id = -1;
+  float w = 0.f;
+  if (!p.skip_routing) {
+    id = route_wave(p, s_bias, tw, w);
+    if (slot_lane) {
+      p.topk_ids[t * kTopK + r] = id;
+      p.topk_w[t * kTopK + r] = w;
+    }
+  } else if (slot_lane) {
+    id = p.topk_ids[t * kTopK + r];
+  }
+  if constexpr (RANKS) {
+    const int le = slot_lane ? local_of(id, p.offset) : -1;
+    const uint64_t m = __ballot(le >= 0);
+    if (r == 0 && t < p.T) p.token_nlocal[t] = __popcll((m >> (lane & 48)) & 0xFFull);
+    if (r < kTopK) s_le[(wave * 4 + (lane >> 4)) * kTopK + r] = le;
+    __syncthreads();
+    // the 128 slots of the work-group are held by threads 0..127 (wavefronts 0 and 1)
+    const int my_le = tid < kRouteTokensPerBlock * kTopK ? s_le[tid] : -1;
+    const int rank = block_rank(my_le, kRouteWaves, s_wcnt, s_cnt);
+    const int slot = blockIdx.x * kRouteTokensPerBlock * kTopK + tid;
+    if (my_le >= 0) p.slot_rank[slot] = rank;
+    if (tid < kExpertsLocal) p.block_count[blockIdx.x * kExpertsLocal + tid] = s_cnt[tid];
+  }
+}
+
+// Dispatch of small batches (T <= kSinglePassTokens) in one work-group, from the top-k
+// lists in the workspace: local counts, stable ranks (1024 slots at a time), CSR offsets,
+// the work list and the placement, without leaving the work-group.
+__global__ __launch_bounds__(kRouteThreads) void dispatch_small_kernel(RouteParams p) {
   __shared__ int s_le[kSinglePassTokens * kTopK];
   __shared__ int s_rank[kSinglePassTokens * kTopK];
   __shared__ float s_w[kSinglePassTokens * kTopK];
@@ -290,20 +321,19 @@ __global__ __launch_bounds__(kRouteThreads) void route_dispatch_small_kernel(Rou
   __shared__ int s_start[kExpertsLocal + 1];
 
   const int tid = threadIdx.x;
-  const int lane = lane_id();
-  const int wave = tid >> 6;
   const int nslots = p.T * kTopK;
-  stage_bias(p, s_bias);
-  for (int t = wave; t < p.T; t += kRouteTokensPerBlock) {
-    float w;
-    const int le = route_or_load(p, s_bias, t, w);
-    if (lane < kTopK) {
-      s_le[t * kTopK + lane] = le;
-      s_w[t * kTopK + lane] = w;
-    }
+  for (int slot = tid; slot < nslots; slot += kRouteThreads) {
+    s_le[slot] = local_of(p.topk_ids[slot], p.offset);
+    s_w[slot] = p.topk_w[slot];
   }
   if (tid < kExpertsLocal) s_base[tid] = 0;
   __syncthreads();
+  for (int t = tid; t < p.T; t += kRouteThreads) {
+    int n = 0;
+#pragma unroll
+    for (int k = 0; k < kTopK; ++k) n += s_le[t * kTopK + k] >= 0 ? 1 : 0;
+    p.token_nlocal[t] = n;
+  }
   for (int c0 = 0; c0 < nslots; c0 += kRouteThreads) {
     const int slot = c0 + tid;
     const int le = slot < nslots ? s_le[slot] : -1;
@@ -323,33 +353,6 @@ __global__ __launch_bounds__(kRouteThreads) void route_dispatch_small_kernel(Rou
     p.sorted_weight[pos] = s_w[slot];
     p.sorted_slot[pos] = slot;
   }
-}
-
-// Large batches, step 1: one wavefront per token; the work-group of 16 tokens records each
-// local slot's stable rank inside the work-group and the work-group's expert histogram.
-__global__ __launch_bounds__(kRouteThreads) void route_count_kernel(RouteParams p) {
-  __shared__ __attribute__((aligned(16))) float s_bias[kExpertsGlobal];
-  __shared__ int s_le[kRouteTokensPerBlock * kTopK];
-  __shared__ int s_wcnt[16][kExpertsLocal];
-  __shared__ int s_cnt[kExpertsLocal];
-  const int tid = threadIdx.x;
-  const int lane = lane_id();
-  const int wave = tid >> 6;
-  const int t = blockIdx.x * kRouteTokensPerBlock + wave;
-  stage_bias(p, s_bias);
-  int le = -1;
-  if (t < p.T) {
-    float w;
-    le = route_or_load(p, s_bias, t, w);
-  }
-  if (lane < kTopK) s_le[wave * kTopK + lane] = le;
-  __syncthreads();
-  // the 128 slots of the work-group are held by threads 0..127 (wavefronts 0 and 1)
-  const int my_le = tid < kRouteTokensPerBlock * kTopK ? s_le[tid] : -1;
-  const int r = block_rank(my_le, kRouteThreads / 64, s_wcnt, s_cnt);
-  const int slot = blockIdx.x * kRouteTokensPerBlock * kTopK + tid;
-  if (my_le >= 0) p.slot_rank[slot] = r;
-  if (tid < kExpertsLocal) p.block_count[blockIdx.x * kExpertsLocal + tid] = s_cnt[tid];
 }
 
 // Large batches, step 2 (one work-group): per-expert exclusive prefix of the work-group
@@ -401,9 +404,11 @@ __global__ __launch_bounds__(kRouteTokensPerBlock * kTopK) void place_kernel(Rou
 
 hipError_t launch_route_dispatch(const RouteParams& p, hipStream_t s) {
   if (p.single_pass) {
-    hipLaunchKernelGGL(route_dispatch_small_kernel, dim3(1), dim3(kRouteThreads), 0, s, p);
+    if (!p.skip_routing)
+      hipLaunchKernelGGL(route_kernel<false>, dim3(p.nblocks), dim3(kRouteWaves * 64), 0, s, p);
+    hipLaunchKernelGGL(dispatch_small_kernel, dim3(1), dim3(kRouteThreads), 0, s, p);
   } else {
-    hipLaunchKernelGGL(route_count_kernel, dim3(p.nblocks), dim3(kRouteThreads), 0, s, p);
+    hipLaunchKernelGGL(route_kernel<true>, dim3(p.nblocks), dim3(kRouteWaves * 64), 0, s, p);
     hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(kRouteThreads), 0, s, p);
     hipLaunchKernelGGL(place_kernel, dim3(p.nblocks), dim3(kRouteTokensPerBlock * kTopK), 0, s, p);
   }
