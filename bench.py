@@ -53,6 +53,8 @@ def parse():
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--weight-sets", type=int, default=3)
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="only run a plain 1 GiB device copy (calibration of rocprofv3 byte counters)")
     return ap.parse_args()
 
 
@@ -144,12 +146,13 @@ def bench_workload(pkg, inputs, name, weight_sets, steps, warmup):
                tflops=round(f["layer_flops"] / (us * 1e-6) / 1e12, 2),
                stage_us=dict(route_dispatch=round(stage_ms[0] * 1e3, 2), gemm1=round(stage_ms[1] * 1e3, 2),
                              gemm2_combine=round(stage_ms[2] * 1e3, 2)))
+    res["rows_per_item"] = int(ws.layout.rows_per_item)
     res["hbm_roofline_frac"] = round(res["hbm_gbs"] / HBM_PEAK_GBS, 4)
     res["mfma_roofline_frac"] = round(res["tflops"] / FP8_PEAK_TFLOPS, 4)
     return res, f, stage_ms, kw
 
 
-def cpu_baseline(kw, weight_set):
+def cpu_baseline(kw, weight_set, reps=5):
     """The numpy oracle (definition mode) on the same workload, timed on this host."""
     import numpy as np
     import torch
@@ -164,18 +167,45 @@ def cpu_baseline(kw, weight_set):
             u8(kw["hidden_states"]), kw["hidden_states_scale"].cpu().numpy(), u8(weight_set[0]),
             weight_set[1].cpu().numpy(), u8(weight_set[2]), weight_set[3].cpu().numpy(),
             kw["local_expert_offset"], kw["routed_scaling_factor"])
-    t0 = time.perf_counter()
-    r = olayer.layer_forward(*args, mode="definition")
-    dt = time.perf_counter() - t0
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        r = olayer.layer_forward(*args, mode="definition")
+        times.append(time.perf_counter() - t0)
+    dt = float(np.median(times))
     T = args[0].shape[0]
     cnt = r["expert_count"]
     n, e_touched = int(cnt.sum()), int((cnt > 0).sum())
     b = e_touched * BYTES_PER_EXPERT + T * BYTES_PER_TOKEN + 512
     return dict(value=round(b / dt / 1e9, 3), unit="GB/s", cores=int(threads), kind="port",
-                sample=f"whole layer, T={T}, {e_touched} touched experts, {n} assignments, one run "
-                       f"of oracle.layer_forward(mode='definition'): {dt:.2f} s "
-                       f"(numpy: BLAS matmuls on {threads} threads, element-wise work on 1)",
+                sample=f"whole layer, T={T}, {e_touched} touched experts, {n} assignments: median of "
+                       f"{reps} runs of oracle.layer_forward(mode='definition'), {dt:.2f} s each, "
+                       f"{sum(times):.1f} s in all (numpy: BLAS matmuls on {threads} threads, "
+                       "element-wise work on 1)",
                 seconds=round(dt, 3), us_per_step=round(dt * 1e6, 1))
+
+
+def traffic_from_profiles(kernel_tag, workload):
+    """HBM bytes per launch of the dominant kernel, from the committed rocprofv3 --pmc
+    summary for this kernel and workload (FETCH_SIZE + WRITE_SIZE per dispatch, scaled by
+    the counters' reading for a plain copy of known size), or None when there is none."""
+    path = ROOT / "profiles" / f"{kernel_tag}_{workload}_traffic.json"
+    if not path.exists():
+        return None
+    return json.loads(path.read_text()).get("hbm_bytes_per_launch")
+
+
+def copy_probe():
+    """A plain device-to-device copy of 1 GiB, five times: the reference point that scales
+    rocprofv3's FETCH_SIZE / WRITE_SIZE readings to bytes."""
+    import torch
+    n = 1 << 30
+    a = torch.ones(n, dtype=torch.uint8, device="cuda:0")
+    b = torch.empty_like(a)
+    for _ in range(5):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_probe_bytes": n, "copies": 5}), flush=True)
 
 
 def main():
@@ -184,6 +214,9 @@ def main():
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
               "(this build runs the layer on a single MI355X).", file=sys.stderr)
         sys.exit(2)
+    if args.copy_probe:
+        copy_probe()
+        return
     import torch
     import __graft_entry__ as ge
     pkg = ge.load_package()
@@ -205,18 +238,26 @@ def main():
 
     m = results[args.workload]
     T = m["T"]
-    # dominant kernel: GEMM1 (W13 is two thirds of the weight bytes) in the HBM-bound regime
-    g1_ms, g2c_ms = main_stage[1], main_stage[2]
+    # Dominant kernel: GEMM1, the one kernel of stage 2 (W13 is two thirds of the weight
+    # bytes); HBM-bound up to T = 1024, MFMA-bound above. Its launch duration is the HIP-event
+    # time of stage 2 on the launch stream.
+    g1_ms = main_stage[1]
+    rpi = m["rows_per_item"]
+    if rpi <= 32:
+        kernel, tag = f"gemm_stream_kernel<1, {1 if rpi <= 16 else 2}>", "gemm1_stream"
+    else:
+        kernel, tag = "gemm_tile_kernel<true, 4>", "gemm1_tile"
     if T <= 1024:
-        roof = dict(kernel="gemm1 (gemm_kernel<1,*>)", bound="hbm", achieved=round(main_f["g1_bytes"] / (g1_ms * 1e-3) / 1e9, 1),
+        roof = dict(kernel=kernel, bound="hbm", achieved=round(main_f["g1_bytes"] / (g1_ms * 1e-3) / 1e9, 1),
                     peak=HBM_PEAK_GBS, unit="GB/s")
     else:
-        roof = dict(kernel="gemm1 (gemm_kernel<1,*>)", bound="mfma",
+        roof = dict(kernel=kernel, bound="mfma",
                     achieved=round(main_f["g1_flops"] / (g1_ms * 1e-3) / 1e12, 2), peak=FP8_PEAK_TFLOPS, unit="TFLOP/s")
     roof["frac"] = round(roof["achieved"] / roof["peak"], 4)
-    roof["traffic"] = None
+    roof["traffic"] = traffic_from_profiles(tag, args.workload)
     roof["avg_launch_us"] = round(g1_ms * 1e3, 2)
     roof["algorithmic_bytes"] = main_f["g1_bytes"]
+    roof["algorithmic_flops"] = main_f["g1_flops"]
 
     cpu = None
     if not args.no_cpu:

@@ -160,15 +160,18 @@ int moe_fp8_run(const moe_fp8_args* args, void* workspace, size_t workspace_byte
 int moe_fp8_route_dispatch(const moe_fp8_args* args, int32_t skip_routing, void* workspace,
                            size_t workspace_bytes, hipStream_t stream);
 
-/* Stage 2: GEMM1 over the gathered tokens of each local expert, SwiGLU (silu of the
- * second half times the first half) and requantisation of the result to fp8 with one
- * scale per row per 128 columns. Reads the dispatch arrays, writes act/act_scale.
+/* Stage 2: GEMM1 over the gathered tokens of each local expert and SwiGLU (silu of the
+ * second half times the first half). One kernel. Reads the dispatch arrays; writes the
+ * fp8 intermediate act/act_scale (one scale per row per 128 columns) when
+ * layout.rows_per_item > 32, otherwise the fp32 SwiGLU rows `swiglu`, which stage 3
+ * requantises first.
  * Replaces the token pack and moe_gemm1_kernel (kernel.py:663-693, 7-151). */
 int moe_fp8_gemm1(const moe_fp8_args* args, void* workspace, size_t workspace_bytes,
                   hipStream_t stream);
 
-/* Stage 3: GEMM2 of act against the expert's down projection, weighting by the routing
- * weight and the deterministic per-token combine into args->output.
+/* Stage 3: (when layout.rows_per_item <= 32) requantisation of the fp32 SwiGLU rows to
+ * act/act_scale; GEMM2 of act against the expert's down projection, weighting by the
+ * routing weight and the deterministic per-token combine into args->output.
  * Replaces moe_gemm2_kernel and the finalize copy (kernel.py:695-729, 153-250). */
 int moe_fp8_gemm2_combine(const moe_fp8_args* args, void* workspace, size_t workspace_bytes,
                           hipStream_t stream);

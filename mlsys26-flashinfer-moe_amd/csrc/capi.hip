@@ -197,6 +197,7 @@ int moe_fp8_gemm2_combine(const moe_fp8_args* args, void* workspace, size_t work
   if (rc != MOE_FP8_OK) return rc;
   if (args->num_tokens == 0) return MOE_FP8_OK;
   const GemmParams p = gemm_params(args, L, workspace);
+  if (launch_requant(p, L.rows_per_item, stream) != hipSuccess) return MOE_FP8_ELAUNCH;
   if (launch_gemm2(p, L.rows_per_item, stream) != hipSuccess) return MOE_FP8_ELAUNCH;
   return launch_combine(p, stream) == hipSuccess ? MOE_FP8_OK : MOE_FP8_ELAUNCH;
 }
@@ -211,6 +212,7 @@ int moe_fp8_run(const moe_fp8_args* args, void* workspace, size_t workspace_byte
   const GemmParams gp = gemm_params(args, L, workspace);
   if (launch_route_dispatch(rp, stream) != hipSuccess) return MOE_FP8_ELAUNCH;
   if (launch_gemm1(gp, L.rows_per_item, stream) != hipSuccess) return MOE_FP8_ELAUNCH;
+  if (launch_requant(gp, L.rows_per_item, stream) != hipSuccess) return MOE_FP8_ELAUNCH;
   if (launch_gemm2(gp, L.rows_per_item, stream) != hipSuccess) return MOE_FP8_ELAUNCH;
   if (launch_combine(gp, stream) != hipSuccess) return MOE_FP8_ELAUNCH;
   return MOE_FP8_OK;

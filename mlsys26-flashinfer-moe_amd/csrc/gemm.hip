@@ -310,9 +310,12 @@ hipError_t launch_stream(const GemmParams& p, int rows_per_item, hipStream_t s) 
 
 hipError_t launch_gemm1(const GemmParams& p, int rows_per_item, hipStream_t s) {
   if (rows_per_item > 32) return launch_gemm1_tile(p, s);
-  const hipError_t e = launch_stream<kG1>(p, rows_per_item, s);
-  if (e != hipSuccess) return e;
-  int grid = p.max_items * rows_per_item;   // >= the number of SwiGLU rows
+  return launch_stream<kG1>(p, rows_per_item, s);
+}
+
+hipError_t launch_requant(const GemmParams& p, int rows_per_item, hipStream_t s) {
+  if (rows_per_item > 32) return hipSuccess;   // the tile GEMM1 requantises in its epilogue
+  int grid = p.max_items * rows_per_item;      // >= the number of SwiGLU rows
   if (grid > num_cus() * 8) grid = num_cus() * 8;
   if (grid > 0) hipLaunchKernelGGL(requant_kernel, dim3(grid), dim3(256), 0, s, p);
   return hipGetLastError();

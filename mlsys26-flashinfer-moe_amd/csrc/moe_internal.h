@@ -4,10 +4,11 @@
 //   caller tensors   : the contract of kernel.py:591-607 (see include/moe_fp8.h)
 //   workspace arrays : moe_fp8_layout offsets; every array is 256-byte aligned.
 // Kernels of one call run in this order on one stream:
-//   route_dispatch_small_kernel | (route_count_kernel -> scan_kernel -> place_kernel)
-//   -> GEMM1 -> GEMM2 -> combine_kernel
-// where, with <= 32 rows per work item, GEMM1 is gemm_stream_kernel<1> + requant_kernel and
-// GEMM2 is gemm_stream_kernel<2>; with more rows both are gemm_tile_kernel.
+//   (route_kernel<false> -> dispatch_small_kernel) | (route_kernel<true> -> scan_kernel -> place_kernel)
+//   -> GEMM1 -> [requant_kernel] -> GEMM2 -> combine_kernel
+// where, with <= 32 rows per work item, the GEMMs are gemm_stream_kernel<1|2> and GEMM1
+// leaves fp32 SwiGLU rows for requant_kernel; with more rows both are gemm_tile_kernel and
+// GEMM1 requantises in its epilogue.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -103,6 +104,7 @@ struct GemmParams {
 
 hipError_t launch_route_dispatch(const RouteParams& p, hipStream_t s);
 hipError_t launch_gemm1(const GemmParams& p, int rows_per_item, hipStream_t s);
+hipError_t launch_requant(const GemmParams& p, int rows_per_item, hipStream_t s);
 hipError_t launch_gemm2(const GemmParams& p, int rows_per_item, hipStream_t s);
 hipError_t launch_combine(const GemmParams& p, hipStream_t s);
 hipError_t launch_gemm1_tile(const GemmParams& p, hipStream_t s);

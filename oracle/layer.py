@@ -55,6 +55,7 @@ def layer_forward(routing_logits, routing_bias, hidden_states, hidden_states_sca
 
     act = np.zeros((n, inter), dtype=np.uint8) if mode == "emulated" else None
     act_scale = np.zeros((n, inter // requant_block), dtype=F32) if mode == "emulated" else None
+    swiglu = np.zeros((n, inter), dtype=F32)  # fp32 SwiGLU row of each assignment
     y = np.zeros((n, H), dtype=F32)          # weighted GEMM2 row of each assignment
     done = np.zeros(n, dtype=bool)
     for e in range(e_local):
@@ -70,6 +71,7 @@ def layer_forward(routing_logits, routing_bias, hidden_states, hidden_states_sca
         w13 = ex.dequant_blocks(gemm1_weights[e], gemm1_weights_scale[e], block)
         c = ex.swiglu(ex.gemm(a, w13), inter)
         del w13
+        swiglu[rows] = c
         if mode == "emulated":
             q, sc = ex.requant_rows(c, requant_block)
             act[rows], act_scale[rows] = q, sc
@@ -100,6 +102,7 @@ def layer_forward(routing_logits, routing_bias, hidden_states, hidden_states_sca
         "topk_ids": ids,
         "topk_weights": wts,
         **d,
+        "swiglu": swiglu,
         "act": act,
         "act_scale": act_scale,
         "rows": y,

@@ -115,6 +115,18 @@ def test_intermediate_fp8_matches_oracle(name):
     emu = olayer.layer_forward(**npkw, mode="emulated")
     n = len(emu["sorted_slot"])
     assert gh.counters(ws)[1] == n
+    if ws.layout.rows_per_item <= 32:
+        # decode regime: stage 2 leaves the fp32 SwiGLU rows, stage 3 requantises them.
+        # GEMM1 outputs differ from the fp32 oracle by the MFMA's block-sum precision,
+        # relative to the row's magnitude.
+        c = gh.read(ws, "swiglu", torch.float32, n * 2048).reshape(n, 2048)
+        ref = emu["swiglu"]
+        row_max = np.max(np.abs(ref), axis=1, keepdims=True)
+        err = np.abs(c - ref)
+        bound = 1e-3 * np.abs(ref) + 2e-4 * row_max
+        print(f"{name}: swiglu max err / bound {np.max(err / bound):.3f}", flush=True)
+        assert np.all(err <= bound)
+    gh.gemm2_combine(args, ws)
     act = gh.read(ws, "act", torch.uint8, n * 2048).reshape(n, 2048)
     sc = gh.read(ws, "act_scale", torch.float32, n * 16).reshape(n, 16)
     # The fp8 MFMA sums each 128-long K block at less than fp32 precision (observed
