@@ -140,8 +140,9 @@ size_t moe_fp8_workspace_bytes(int32_t num_tokens);
 int moe_fp8_workspace_layout(int32_t num_tokens, moe_fp8_layout* layout);
 
 /* Clears the workspace's control block. A freshly allocated workspace must be passed
- * through this once before its first use; every later call leaves the control block
- * cleared again, so one workspace is reusable by successive calls on one stream.
+ * through this once before its first use (so that a GEMM stage run before any dispatch
+ * finds no work); every dispatch rewrites the control block before the GEMMs read it,
+ * so one workspace is reusable by successive calls on one stream without clearing.
  * Calls that overlap in time must use different workspaces. No counterpart in the
  * reference, whose temporaries are freshly zeroed torch tensors (kernel.py:348, 669-670, 704). */
 int moe_fp8_workspace_init(void* workspace, size_t workspace_bytes, hipStream_t stream);

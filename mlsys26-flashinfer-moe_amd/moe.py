@@ -66,7 +66,7 @@ def validate(routing_logits, routing_bias, hidden_states, hidden_states_scale, g
 class Workspace:
     """A device workspace for the C ABI, initialised once with moe_fp8_workspace_init.
 
-    The library leaves the control block cleared after every call, so one workspace
+    Every dispatch rewrites the control block before the GEMMs read it, so one workspace
     serves any number of successive calls issued on one stream.
     """
 
