@@ -98,7 +98,8 @@ typedef struct moe_fp8_args {
  *   sorted_weight fp32  [N_max]     routing weight of each assignment               (kernel.py:365)
  *   sorted_slot   int32 [N_max]     flat slot t*8+k of each assignment
  *   token_nlocal  int32 [T]         number of local assignments of each token
- *   work_items    int32 [max_items, 4]  GEMM work list (expert, first row, rows, 0)  (kernel.py:384-407)
+ *   work_items    int32 [max_items, 4]  GEMM work list (expert, first row, rows,
+ *                                   first item of the expert | its item count << 16) (kernel.py:384-407)
  *   counters      int32 [16]        [0] number of work items, [1] N; the rest reserved
  *   act           fp8   [N_max, 2048]    SwiGLU output requantised to e4m3fn          (kernel.py:669)
  *   act_scale     fp32  [N_max, 16]      its 1x128 block scales, row-major per row   (kernel.py:670)

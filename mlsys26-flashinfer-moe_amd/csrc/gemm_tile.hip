@@ -1,23 +1,25 @@
 // Large-batch grouped fp8 block-scale GEMMs of the MoE layer (gfx950 MFMA).
 //
-// Tile = (work item of <= 128 assignment rows of one local expert) x (WAVES*64 weight rows).
-// Each wavefront of the work-group owns 64 weight rows (four 16-row MFMA fragments) against
-// all rows of the item, i.e. 4 x NG v_mfma_f32_16x16x128_f8f6f4 per 128-wide K-step with
-// 16*NG fp32 accumulators per lane (NG = row groups of 16 in the item; the K loop is
-// instantiated per NG so that it carries no per-group branches).
-//   GEMM1: wavefront w owns SwiGLU columns [32w, 32w+32) of the tile: gate rows and the
-//          matching up rows (fragments 0,1 and 2,3).
-//   GEMM2: wavefront w owns hidden rows [64w, 64w+64) of the tile.
-// Activations (gathered by token for GEMM1, contiguous for GEMM2) and their per-K-block
-// scales flow through a 3-stage LDS ring filled with global_load_lds (no VGPR staging),
-// two K-steps ahead; weights stream straight into a 2-stage VGPR ring, one K-step ahead.
-// The waits are explicit: at the top of step k every wave waits until only the ring
-// loads of step k+1 are in flight (s_waitcnt vmcnt), then a raw s_barrier publishes the
-// LDS stage of step k. Each K-step is one 128x128 scale block: acc += mfma * (s_a * s_w)
-// (kernel.py:123-124, :234).
+// Tile = (work item of <= 128 assignment rows of one local expert) x (256 weight rows).
+// A work-group of 8 wavefronts (two per SIMD) computes one tile; wavefront w = 4a + b owns
+// weight rows [64b, 64b+64) of the tile (four 16-row MFMA fragments) against item rows
+// [64a, 64a+64) (up to four 16-row groups): 4 x NG v_mfma_f32_16x16x128_f8f6f4 per 128-wide
+// K-step with 16*NG fp32 accumulators per lane.
+//   GEMM1: the tile is 128 SwiGLU columns: tile rows 0..127 are their gate rows of W13,
+//          rows 128..255 the matching up rows; wavefront (a, b) owns columns [32b, 32b+32)
+//          (fragments 0,1 gate, 2,3 up).
+//   GEMM2: the tile is 256 hidden rows of W2.
+// Both operands of a K-step (256 x 128 weight bytes, 128 x 128 activation bytes and the
+// activations' scales) flow through a 3-stage LDS ring filled with global_load_lds two
+// K-steps ahead: every 16-byte DMA instruction reads 8 whole 128-byte rows, so the vector
+// memory pipeline sees full cache lines. The waits are explicit: at the top of step k every
+// wave waits until only its loads of step k+1 are in flight (s_waitcnt vmcnt), then a raw
+// s_barrier publishes stage k. Each K-step is one 128x128 scale block:
+// acc += mfma * (s_a * s_w) (kernel.py:123-124, :234). With two wavefronts per SIMD, one
+// wavefront's fp32 scale FMAs overlap the other's MFMAs.
 //
-// LDS activation tile: 16-byte chunk c of row m lives at m*128 + ((c ^ ((m >> 1) & 7)) * 16),
-// which spreads the 16 rows read by one ds_read_b128 across distinct bank groups.
+// LDS tiles: 16-byte chunk c of row m lives at m*128 + ((c ^ ((m >> 1) & 7)) * 16), which
+// spreads the 16 rows read by one ds_read_b128 across distinct bank groups.
 //
 // Scheduling: the work units (item, tile) of expert e are numbered tile-major
 // (all items of one weight tile are consecutive) and dealt to the 8 XCDs in contiguous
@@ -29,8 +31,13 @@ namespace moe {
 
 namespace {
 
-constexpr int kTileRows = 128;   // LDS activation tile rows (max rows of a work item)
-constexpr int kTileWaves = 4;    // wavefronts per work-group (one per SIMD)
+constexpr int kTileRows = 128;                       // item rows per tile (max rows of an item)
+constexpr int kTileW = 256;                          // weight rows per tile
+constexpr int kTileWaves = 8;                        // wavefronts per work-group
+constexpr int kStages = 3;                           // LDS ring stages
+constexpr int kWDma = kTileW / kTileWaves / 8;       // weight DMA loads per wavefront per step (4)
+constexpr int kADma = kTileRows / kTileWaves / 8;    // activation DMA loads per wavefront per step (2)
+constexpr int kLoadsPerStep = kWDma + kADma + 1;     // + 1 scale DMA
 
 typedef __attribute__((address_space(3))) void lds_void;
 
@@ -61,171 +68,168 @@ __device__ __forceinline__ void ring_barrier() {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
-__device__ __forceinline__ v8i load_frag(const uint8_t* p) {
-  const v4i lo = *reinterpret_cast<const v4i*>(p);
-  const v4i hi = *reinterpret_cast<const v4i*>(p + 64);
-  return join(lo, hi);
-}
-
-constexpr int kStages = 4;       // LDS ring stages (4 divides both K-step counts, 56 and 16)
-
-template <int WAVES>
-struct TileShared {
-  uint8_t a[kStages][kTileRows * 128];
-  float sa[kStages][WAVES * 64];   // row m at (m / DMA_ROWS) * 64 + m % DMA_ROWS
-  float amax[WAVES][kTileRows];
+struct TileStage {
+  uint8_t w[kTileW * 128];
+  uint8_t a[kTileRows * 128];
+  float sa[kTileWaves * 64];   // scale of item row m at (m / 16) * 64 + m % 16
 };
 
-template <int V>
-struct IntC {
-  static constexpr int value = V;
+struct TileShared {
+  TileStage st[kStages];
+  float amax[4][kTileRows];
 };
 
 // Per-work-unit pointers of one lane.
-template <int NDMA>
 struct TileCtx {
-  const uint8_t* asrc[NDMA];  // activation DMA sources (row + permuted 16-byte chunk)
-  const float* ssrc;          // activation scale DMA source
-  size_t sstride;             // scale stride between K blocks
-  const uint8_t* wp[4];       // weight fragment rows
-  const float* swp0;          // block scales of fragments 0,1 (GEMM1 gate) ...
-  const float* swp1;          // ... and 2,3 (GEMM1 up)
+  const uint8_t* wsrc[kWDma];  // weight DMA sources (row + permuted 16-byte chunk)
+  const uint8_t* asrc[kADma];  // activation DMA sources
+  const float* ssrc;           // activation scale DMA source
+  size_t sstride;              // scale stride between K blocks
+  const float* swp0;           // block scales of fragments 0,1 (GEMM1 gate) ...
+  const float* swp1;           // ... and 2,3 (GEMM1 up)
   int r0, rows, tile;
 };
 
-template <bool G1, int WAVES, int NG>
-__device__ __forceinline__ void tile_body(const GemmParams& p, const TileCtx<kTileRows / WAVES / 8>& c,
-                                          TileShared<WAVES>& sh) {
+// A 16-row MFMA operand fragment (rows m0 .. m0+15 of an LDS tile): lane l holds row
+// m0 + l%16, chunks l/16 and 4 + l/16.
+__device__ __forceinline__ v8i lds_frag(const uint8_t* buf, int m, int lane) {
+  return join(*reinterpret_cast<const v4i*>(buf + swz(m, lane >> 4)),
+              *reinterpret_cast<const v4i*>(buf + swz(m, 4 + (lane >> 4))));
+}
+
+template <bool G1, int NG>
+__device__ __forceinline__ void tile_body(const GemmParams& p, const TileCtx& c, TileShared& sh) {
   constexpr int KS = G1 ? kHBlocks : kIBlocks;
-  constexpr int TILE_W = WAVES * 64;
-  constexpr int DMA_ROWS = kTileRows / WAVES;
-  constexpr int NDMA = DMA_ROWS / 8;
-  constexpr int DMA_PER_STEP = NDMA + 1;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wb = wave & 3, wa = wave >> 2;   // weight rows 64*wb.., item rows 64*wa..
 
-  // every lane of the wave loads (lanes >= DMA_ROWS repeat a row into unused slots), so
-  // the loads carry no divergent control flow
-  auto issue_a = [&](int k, int stage) {
-#pragma unroll
-    for (int j = 0; j < NDMA; ++j)
-      dma16(c.asrc[j] + k * 128, &sh.a[stage][(DMA_ROWS * wave + 8 * j) * 128]);
-    dma4(c.ssrc + k * c.sstride, &sh.sa[stage][64 * wave]);
-  };
   // lane k holds the weight block scales of K-step k (read back with readlane: the loop
   // itself touches no memory for them)
   const float sw0_lane = c.swp0[lane < KS ? lane : 0];
   const float sw1_lane = c.swp1[lane < KS ? lane : 0];
-  v8i wr[2][4];
-  auto load_w = [&](int k, v8i (&dst)[4]) {
+
+  // Loads of step k into stage s: this wave's share of the weight rows, activation rows and
+  // activation scales. Every lane loads (lanes past the wave's 16 scale rows repeat them
+  // into unused slots), so no load is divergent; every wave loads even if it has no rows.
+  auto issue = [&](int k, int s) {
+    TileStage& st = sh.st[s];
 #pragma unroll
-    for (int f = 0; f < 4; ++f) dst[f] = load_frag(c.wp[f] + k * 128);
+    for (int j = 0; j < kWDma; ++j) dma16(c.wsrc[j] + k * 128, &st.w[(32 * wave + 8 * j) * 128]);
+#pragma unroll
+    for (int j = 0; j < kADma; ++j) dma16(c.asrc[j] + k * 128, &st.a[(16 * wave + 8 * j) * 128]);
+    dma4(c.ssrc + k * c.sstride, &st.sa[64 * wave]);
   };
-  v4f acc[4][NG];
+
+  v4f acc[4][NG > 0 ? NG : 1];
 #pragma unroll
   for (int f = 0; f < 4; ++f)
 #pragma unroll
     for (int g = 0; g < NG; ++g) acc[f][g] = v4f{0.f, 0.f, 0.f, 0.f};
   const v4f zero = {0.f, 0.f, 0.f, 0.f};
 
-  auto compute = [&](int stage, const v8i (&wf)[4], float s0, float s1) {
-    const uint8_t* abuf = sh.a[stage];
-    const float* sbuf = sh.sa[stage];
-    const int c0 = lane >> 4, c1 = 4 + (lane >> 4);
-#pragma unroll
-    for (int g = 0; g < NG; ++g) {
-      const int m = g * 16 + (lane & 15);
-      const v8i bf = join(*reinterpret_cast<const v4i*>(abuf + swz(m, c0)),
-                          *reinterpret_cast<const v4i*>(abuf + swz(m, c1)));
-      const float sa = sbuf[(m / DMA_ROWS) * 64 + m % DMA_ROWS];
-      const float f0 = sa * s0, f1 = sa * s1;
-      v4f d[4];
-#pragma unroll
-      for (int f = 0; f < 4; ++f) d[f] = mfma16x16x128_fp8(wf[f], bf, zero);
-#pragma unroll
-      for (int f = 0; f < 4; ++f) acc[f][g] += d[f] * (f < 2 ? f0 : f1);
-      // one row group's MFMA results live at a time (the scheduler would otherwise hoist
-      // every MFMA of the step and hold all their results)
-      __builtin_amdgcn_sched_barrier(0);
-    }
+  // weight fragment f of this wave: GEMM1 gate rows 32*wb + 16f (f = 0,1) and the up rows
+  // 128 + 32*wb + 16(f-2) (f = 2,3); GEMM2 rows 64*wb + 16f
+  auto wrow = [&](int f) {
+    if constexpr (G1) return (f < 2 ? 32 * wb + 16 * f : 128 + 32 * wb + 16 * (f - 2)) + (lane & 15);
+    else return 64 * wb + 16 * f + (lane & 15);
   };
 
-  // One K-step. Issue order per step: weights of step k+1, then activations of step
-  // k+3, so that at the top of step k only step k+2's activation loads may be in flight.
-  // Every step has the same shape: past the last step, the loads repeat the last step's
-  // data (cache-hot) into ring slots that are never read.
-  auto step = [&](int k, auto UU) {
-    constexpr int uu = decltype(UU)::value;   // k % 4
-    ring_barrier<DMA_PER_STEP>();
-    load_w(min(k + 1, KS - 1), wr[(uu + 1) & 1]);
-    issue_a(min(k + 3, KS - 1), (uu + 3) % kStages);
-    const float s0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sw0_lane), k));
-    const float s1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sw1_lane), k));
-    compute(uu, wr[uu & 1], s0, s1);
+  auto compute = [&](int s, float s0, float s1) {
+    if constexpr (NG > 0) {
+      const TileStage& st = sh.st[s];
+      v8i wf[4];
+#pragma unroll
+      for (int f = 0; f < 4; ++f) wf[f] = lds_frag(st.w, wrow(f), lane);
+      v8i bf = lds_frag(st.a, 64 * wa + (lane & 15), lane);
+      float sa = st.sa[(4 * wa) * 64 + (lane & 15)];
+#pragma unroll
+      for (int g = 0; g < NG; ++g) {
+        // the next row group's fragment is read from LDS while this group's MFMAs run
+        v8i bf_next = bf;
+        float sa_next = sa;
+        if (g + 1 < NG) {
+          bf_next = lds_frag(st.a, 64 * wa + 16 * (g + 1) + (lane & 15), lane);
+          sa_next = st.sa[(4 * wa + g + 1) * 64 + (lane & 15)];
+        }
+        v4f d[4];
+#pragma unroll
+        for (int f = 0; f < 4; ++f) d[f] = mfma16x16x128_fp8(wf[f], bf, zero);
+        const float f0 = sa * s0, f1 = sa * s1;
+#pragma unroll
+        for (int f = 0; f < 4; ++f) acc[f][g] += d[f] * (f < 2 ? f0 : f1);
+        // one row group's MFMA results live at a time (the scheduler would otherwise hoist
+        // every MFMA of the step and hold all their results)
+        __builtin_amdgcn_sched_barrier(0);
+        bf = bf_next;
+        sa = sa_next;
+      }
+    }
   };
 
   // the previous unit's readers of the LDS ring are done before it is refilled
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   __builtin_amdgcn_s_barrier();
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  issue_a(0, 0);
-  issue_a(1, 1);
-  issue_a(2, 2);
-  load_w(0, wr[0]);
-  // the vmcnt wait at step 0 (DMA_PER_STEP outstanding) then also covers stages 0 and 1
-  static_assert(KS % kStages == 0, "K-step count");
+  issue(0, 0);
+  issue(1, 1);
+  int s_cur = 0, s_next = 2;
 #pragma nounroll
-  for (int k0 = 0; k0 < KS; k0 += kStages) {
-    step(k0 + 0, IntC<0>{});
-    step(k0 + 1, IntC<1>{});
-    step(k0 + 2, IntC<2>{});
-    step(k0 + 3, IntC<3>{});
+  for (int k = 0; k < KS; ++k) {
+    // step k's loads are complete for this wave (only step k+1's may be in flight), and
+    // after the barrier for every wave; every wave is also done with stage s_next (step k-1)
+    ring_barrier<kLoadsPerStep>();
+    issue(min(k + 2, KS - 1), s_next);   // past the last step: the last step again, never read
+    __builtin_amdgcn_sched_barrier(0);
+    const float s0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sw0_lane), k));
+    const float s1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sw1_lane), k));
+    compute(s_cur, s0, s1);
+    s_cur = s_cur == kStages - 1 ? 0 : s_cur + 1;
+    s_next = s_next == kStages - 1 ? 0 : s_next + 1;
   }
   // no ring load of this unit may land after the next unit starts refilling the ring
   wait_vmcnt<0>();
 
   if constexpr (G1) {
-    // SwiGLU (kernel.py:126-129) and 1x128 requantisation (kernel.py:131-135 with 128 columns).
-    // Pass 1 publishes each row's amax over this wave's 32 columns; pass 2 recomputes the
-    // SwiGLU values (cheaper than keeping them live) and quantises with the block scale.
-    auto swiglu = [&](int h, int g, int i) {
-      const float x1 = acc[h][g][i], x2 = acc[2 + h][g][i];
-      return (x2 / (1.0f + __expf(-x2))) * x1;
-    };
+    // SwiGLU (kernel.py:126-129) and 1x128 requantisation (kernel.py:131-135 with 128
+    // columns): the tile's 128 columns are one scale block, spread over the 4 wavefronts
+    // that share this wave's item rows.
+    float cval[NG > 0 ? NG : 1][2][4];
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
       float amax = 0.f;
 #pragma unroll
       for (int h = 0; h < 2; ++h)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) amax = fmaxf(amax, fabsf(swiglu(h, g, i)));
+        for (int i = 0; i < 4; ++i) {
+          const float x1 = acc[h][g][i], x2 = acc[2 + h][g][i];
+          cval[g][h][i] = (x2 / (1.0f + __expf(-x2))) * x1;
+          amax = fmaxf(amax, fabsf(cval[g][h][i]));
+        }
       amax = fmaxf(amax, __shfl_xor(amax, 16));
       amax = fmaxf(amax, __shfl_xor(amax, 32));
-      if (lane < 16) sh.amax[wave][g * 16 + lane] = amax;
+      if (lane < 16) sh.amax[wb][64 * wa + 16 * g + lane] = amax;
     }
     __syncthreads();
-    const int wb = wave & ~3;   // the 4 wavefronts sharing a 128-column scale block
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
-      const int m = g * 16 + (lane & 15);
-      const float amax = fmaxf(fmaxf(sh.amax[wb][m], sh.amax[wb + 1][m]), fmaxf(sh.amax[wb + 2][m], sh.amax[wb + 3][m]));
+      const int m = 64 * wa + 16 * g + (lane & 15);
+      const float amax = fmaxf(fmaxf(sh.amax[0][m], sh.amax[1][m]), fmaxf(sh.amax[2][m], sh.amax[3][m]));
       const float scale = fmaxf(amax / 448.0f, 1e-12f);
       if (m < c.rows) {
-        const int col = c.tile * (TILE_W / 2) + wave * 32;
-        uint8_t* dst = p.act + (size_t)(c.r0 + m) * kInter + col + 4 * (lane >> 4);
+        uint8_t* dst = p.act + (size_t)(c.r0 + m) * kInter + c.tile * 128 + 32 * wb + 4 * (lane >> 4);
 #pragma unroll
         for (int h = 0; h < 2; ++h)
           *reinterpret_cast<uint32_t*>(dst + 16 * h) =
-              pack_fp8x4(swiglu(h, g, 0) / scale, swiglu(h, g, 1) / scale, swiglu(h, g, 2) / scale,
-                         swiglu(h, g, 3) / scale);
-        if ((wave & 3) == 0 && lane < 16) p.act_scale[(size_t)(c.r0 + m) * kIBlocks + col / 128] = scale;
+              pack_fp8x4(cval[g][h][0] / scale, cval[g][h][1] / scale, cval[g][h][2] / scale, cval[g][h][3] / scale);
+        if (wb == 0 && lane < 16) p.act_scale[(size_t)(c.r0 + m) * kIBlocks + c.tile] = scale;
       }
     }
     __syncthreads();
   } else {
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
-      const int m = g * 16 + (lane & 15);
+      const int m = 64 * wa + 16 * g + (lane & 15);
       if (m < c.rows) {
         const int pr = c.r0 + m;
         const int t = p.sorted_token[pr];
@@ -235,7 +239,7 @@ __device__ __forceinline__ void tile_body(const GemmParams& p, const TileCtx<kTi
 #pragma unroll
         for (int f = 0; f < 4; ++f) {
           const v4f val = acc[f][g] * wt;
-          const int h = c.tile * TILE_W + wave * 64 + f * 16 + 4 * (lane >> 4);
+          const int h = c.tile * kTileW + 64 * wb + 16 * f + 4 * (lane >> 4);
           if (direct) {
             if (p.out_dtype == MOE_FP8_OUT_BF16)
               *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(p.out) + (size_t)t * kHidden + h) =
@@ -251,14 +255,10 @@ __device__ __forceinline__ void tile_body(const GemmParams& p, const TileCtx<kTi
   }
 }
 
-template <bool G1, int WAVES>
-__global__ __launch_bounds__(WAVES * 64, 1) void gemm_tile_kernel(GemmParams p) {
-  constexpr int TILE_W = WAVES * 64;
-  constexpr int TILES = (G1 ? 2 * kInter : kHidden) / TILE_W;
-  constexpr int DMA_ROWS = kTileRows / WAVES;
-  constexpr int NDMA = DMA_ROWS / 8;
-  static_assert(DMA_ROWS <= 64 && NDMA >= 1, "activation loader shape");
-  __shared__ __attribute__((aligned(1024))) TileShared<WAVES> sh;
+template <bool G1>
+__global__ __launch_bounds__(kTileWaves * 64, 1) void gemm_tile_kernel(GemmParams p) {
+  constexpr int TILES = (G1 ? 2 * kInter : kHidden) / kTileW;
+  __shared__ __attribute__((aligned(1024))) TileShared sh;
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -277,16 +277,25 @@ __global__ __launch_bounds__(WAVES * 64, 1) void gemm_tile_kernel(GemmParams p) 
     // work-item fields are wave-uniform; say so, so that everything derived from them
     // (notably the weight block-scale addresses) stays in scalar registers
     const int e = __builtin_amdgcn_readfirstlane(it.x);
-    TileCtx<NDMA> c;
+    TileCtx c;
     c.r0 = __builtin_amdgcn_readfirstlane(it.y);
     c.rows = __builtin_amdgcn_readfirstlane(it.z);
     c.tile = __builtin_amdgcn_readfirstlane(v / ne);
 
-    // activation DMA: load j of this wave fills LDS rows DMA_ROWS*w + 8j .. +8, lane l
-    // writing row +l/8, physical chunk l%8 (rows past the item's end repeat its first row)
+    // DMA j of this wave fills 8 tile rows, lane l writing row +l/8, physical chunk l%8
+    // (activation rows past the item's end repeat its first row)
 #pragma unroll
-    for (int j = 0; j < NDMA; ++j) {
-      const int m = DMA_ROWS * wave + 8 * j + (lane >> 3);
+    for (int j = 0; j < kWDma; ++j) {
+      const int r = 32 * wave + 8 * j + (lane >> 3);
+      const int ch = (lane & 7) ^ ((r >> 1) & 7);
+      size_t grow;
+      if constexpr (G1) grow = (size_t)e * 2 * kInter + (r < 128 ? c.tile * 128 + r : kInter + c.tile * 128 + r - 128);
+      else grow = (size_t)e * kHidden + c.tile * kTileW + r;
+      c.wsrc[j] = (G1 ? p.w13 : p.w2) + grow * (G1 ? kHidden : kInter) + ch * 16;
+    }
+#pragma unroll
+    for (int j = 0; j < kADma; ++j) {
+      const int m = 16 * wave + 8 * j + (lane >> 3);
       const int mm = m < c.rows ? m : 0;
       const int ch = (lane & 7) ^ ((m >> 1) & 7);
       size_t row;
@@ -295,39 +304,28 @@ __global__ __launch_bounds__(WAVES * 64, 1) void gemm_tile_kernel(GemmParams p) 
       c.asrc[j] = (G1 ? p.hidden : p.act) + row + ch * 16;
     }
     {
-      const int m = DMA_ROWS * wave + (lane % DMA_ROWS);
+      const int m = 16 * wave + (lane & 15);
       const int mm = m < c.rows ? m : 0;
       if constexpr (G1) c.ssrc = p.hidden_scale + p.sorted_token[c.r0 + mm];
       else c.ssrc = p.act_scale + (size_t)(c.r0 + mm) * kIBlocks;
       c.sstride = G1 ? (size_t)p.T : 1;
     }
     if constexpr (G1) {
-      const int row = c.tile * (TILE_W / 2) + wave * 32 + (lane & 15);   // gate row; up = +I
-      const uint8_t* base = p.w13 + ((size_t)e * 2 * kInter + row) * kHidden + (lane >> 4) * 16;
-      c.wp[0] = base;
-      c.wp[1] = base + (size_t)16 * kHidden;
-      c.wp[2] = base + (size_t)kInter * kHidden;
-      c.wp[3] = base + (size_t)(kInter + 16) * kHidden;
-      const int blk = (c.tile * (TILE_W / 2) + wave * 32) / 128;
-      c.swp0 = p.w13_scale + ((size_t)e * 32 + blk) * kHBlocks;
-      c.swp1 = p.w13_scale + ((size_t)e * 32 + kIBlocks + blk) * kHBlocks;
+      c.swp0 = p.w13_scale + ((size_t)e * 32 + c.tile) * kHBlocks;
+      c.swp1 = p.w13_scale + ((size_t)e * 32 + kIBlocks + c.tile) * kHBlocks;
     } else {
-      const int row = c.tile * TILE_W + wave * 64 + (lane & 15);
-      const uint8_t* base = p.w2 + ((size_t)e * kHidden + row) * kInter + (lane >> 4) * 16;
-#pragma unroll
-      for (int f = 0; f < 4; ++f) c.wp[f] = base + (size_t)(16 * f) * kInter;
-      c.swp0 = p.w2_scale + ((size_t)e * kHBlocks + (c.tile * TILE_W + wave * 64) / 128) * kIBlocks;
+      c.swp0 = p.w2_scale + ((size_t)e * kHBlocks + (c.tile * kTileW + 64 * (wave & 3)) / 128) * kIBlocks;
       c.swp1 = c.swp0;
     }
-    switch ((c.rows + 15) >> 4) {
-      case 1: tile_body<G1, WAVES, 1>(p, c, sh); break;
-      case 2: tile_body<G1, WAVES, 2>(p, c, sh); break;
-      case 3: tile_body<G1, WAVES, 3>(p, c, sh); break;
-      case 4: tile_body<G1, WAVES, 4>(p, c, sh); break;
-      case 5: tile_body<G1, WAVES, 5>(p, c, sh); break;
-      case 6: tile_body<G1, WAVES, 6>(p, c, sh); break;
-      case 7: tile_body<G1, WAVES, 7>(p, c, sh); break;
-      default: tile_body<G1, WAVES, 8>(p, c, sh); break;
+    // row groups of this wave's 64 item rows
+    const int mine = c.rows - 64 * (wave >> 2);
+    const int ng = mine <= 0 ? 0 : min(4, (mine + 15) >> 4);
+    switch (ng) {
+      case 0: tile_body<G1, 0>(p, c, sh); break;
+      case 1: tile_body<G1, 1>(p, c, sh); break;
+      case 2: tile_body<G1, 2>(p, c, sh); break;
+      case 3: tile_body<G1, 3>(p, c, sh); break;
+      default: tile_body<G1, 4>(p, c, sh); break;
     }
   }
 }
@@ -346,13 +344,13 @@ int num_cus_tile() {
 
 template <bool G1>
 hipError_t launch_tile(const GemmParams& p, hipStream_t s) {
-  const int tiles = (G1 ? 2 * kInter : kHidden) / (kTileWaves * 64);
+  const int tiles = (G1 ? 2 * kInter : kHidden) / kTileW;
   const int max_units = p.max_items * tiles;
   int grid = (num_cus_tile() + 7) & ~7;
   const int cap = ((max_units + 7) / 8) * 8;
   if (grid > cap) grid = cap;
   if (grid <= 0) return hipSuccess;
-  hipLaunchKernelGGL((gemm_tile_kernel<G1, kTileWaves>), dim3(grid), dim3(kTileWaves * 64), 0, s, p);
+  hipLaunchKernelGGL((gemm_tile_kernel<G1>), dim3(grid), dim3(kTileWaves * 64), 0, s, p);
   return hipGetLastError();
 }
 
