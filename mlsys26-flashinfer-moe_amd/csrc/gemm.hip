@@ -239,26 +239,39 @@ __global__ __launch_bounds__(256) void requant_kernel(GemmParams p) {
 }
 
 // Output rows of every token without exactly one local assignment: the sum of its parked
-// GEMM2 rows in top-k slot order, or zeros. One thread per 4 columns of one token row.
+// GEMM2 rows in top-k slot order, or zeros. One wavefront per (token, 1/7 of the row): the
+// token's local slots become a uniform bit mask, and each lane sums 4 columns in 4 places.
+constexpr int kCombineChunks = 7;   // 1792 float4 per row = 7 chunks x 4 x 64 lanes
+
 __global__ __launch_bounds__(256) void combine_kernel(GemmParams p) {
-  constexpr int kVecPerRow = kHidden / 4;   // 1792
-  const size_t total = (size_t)p.T * kVecPerRow;
-  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
-    const int t = (int)(i / kVecPerRow);
-    const int h4 = (int)(i - (size_t)t * kVecPerRow);
-    if (p.token_nlocal[t] == 1) continue;
-    v4f acc = {0.f, 0.f, 0.f, 0.f};
-    const v4f* rows = reinterpret_cast<const v4f*>(p.partial + (size_t)t * kTopK * kHidden);
+  constexpr int kVecPerRow = kHidden / 4;
+  constexpr int kPerLane = kVecPerRow / kCombineChunks / 64;   // 4
+  const int lane = threadIdx.x & 63;
+  const int nwaves = gridDim.x * 4;
+  const int items = p.T * kCombineChunks;
+  for (int it = blockIdx.x * 4 + (threadIdx.x >> 6); it < items; it += nwaves) {
+    const int t = it / kCombineChunks, ch = it - t * kCombineChunks;
+    if (__builtin_amdgcn_readfirstlane(p.token_nlocal[t]) == 1) continue;
+    const int le = lane < kTopK ? p.topk_ids[t * kTopK + lane] - p.offset : -1;
+    const uint32_t mask = (uint32_t)__ballot(le >= 0 && le < kExpertsLocal);
+    const int v0 = ch * kPerLane * 64 + lane;
+    const v4f* rows = reinterpret_cast<const v4f*>(p.partial + (size_t)t * kTopK * kHidden) + v0;
+    v4f acc[kPerLane];
 #pragma unroll
-    for (int k = 0; k < kTopK; ++k) {
-      const int le = p.topk_ids[t * kTopK + k] - p.offset;
-      if (le >= 0 && le < kExpertsLocal) acc += rows[(size_t)k * kVecPerRow + h4];
+    for (int u = 0; u < kPerLane; ++u) acc[u] = v4f{0.f, 0.f, 0.f, 0.f};
+    for (uint32_t m = mask; m; m &= m - 1) {
+      const v4f* r = rows + (size_t)__builtin_ctz(m) * kVecPerRow;
+#pragma unroll
+      for (int u = 0; u < kPerLane; ++u) acc[u] += r[64 * u];
     }
-    if (p.out_dtype == MOE_FP8_OUT_BF16)
-      reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(p.out) + (size_t)t * kHidden)[h4] =
-          pack_bf16x4(acc[0], acc[1], acc[2], acc[3]);
-    else
-      reinterpret_cast<v4f*>(reinterpret_cast<float*>(p.out) + (size_t)t * kHidden)[h4] = acc;
+#pragma unroll
+    for (int u = 0; u < kPerLane; ++u) {
+      const size_t h4 = (size_t)t * kVecPerRow + v0 + 64 * u;
+      if (p.out_dtype == MOE_FP8_OUT_BF16)
+        reinterpret_cast<uint2*>(p.out)[h4] = pack_bf16x4(acc[u][0], acc[u][1], acc[u][2], acc[u][3]);
+      else
+        reinterpret_cast<v4f*>(p.out)[h4] = acc[u];
+    }
   }
 }
 
@@ -328,11 +341,9 @@ hipError_t launch_gemm2(const GemmParams& p, int rows_per_item, hipStream_t s) {
 
 hipError_t launch_combine(const GemmParams& p, hipStream_t s) {
   if (p.T <= 0) return hipSuccess;
-  const size_t total = (size_t)p.T * (kHidden / 4);
-  size_t grid = (total + 255) / 256;
-  const size_t cap = (size_t)num_cus() * 8;
-  if (grid > cap) grid = cap;
-  hipLaunchKernelGGL(combine_kernel, dim3((unsigned)grid), dim3(256), 0, s, p);
+  int grid = (p.T * kCombineChunks + 3) / 4;   // 4 (token, chunk) items per work-group at a time
+  if (grid > num_cus() * 8) grid = num_cus() * 8;
+  hipLaunchKernelGGL(combine_kernel, dim3(grid), dim3(256), 0, s, p);
   return hipGetLastError();
 }
 

@@ -16,7 +16,8 @@
 // wave waits until only its loads of step k+1 are in flight (s_waitcnt vmcnt), then a raw
 // s_barrier publishes stage k. Each K-step is one 128x128 scale block:
 // acc += mfma * (s_a * s_w) (kernel.py:123-124, :234). With two wavefronts per SIMD, one
-// wavefront's fp32 scale FMAs overlap the other's MFMAs.
+// wavefront's LDS reads and waits overlap the other's MFMAs. (VALU and MFMA issue largely
+// serialise on gfx950: the four scale FMAs per MFMA bound the loop near 65% of MFMA peak.)
 //
 // LDS tiles: 16-byte chunk c of row m lives at m*128 + ((c ^ ((m >> 1) & 7)) * 16), which
 // spreads the 16 rows read by one ds_read_b128 across distinct bank groups.
@@ -81,7 +82,8 @@ struct TileShared {
 
 // Per-work-unit pointers of one lane.
 struct TileCtx {
-  const uint8_t* wsrc[kWDma];  // weight DMA sources (row + permuted 16-byte chunk)
+  const uint8_t* wbase;        // weight tensor (the per-step source is wbase + k*128 + woff)
+  uint32_t woff[kWDma];        // weight DMA byte offsets (row + permuted 16-byte chunk); < 2^30
   const uint8_t* asrc[kADma];  // activation DMA sources
   const float* ssrc;           // activation scale DMA source
   size_t sstride;              // scale stride between K blocks
@@ -115,7 +117,7 @@ __device__ __forceinline__ void tile_body(const GemmParams& p, const TileCtx& c,
   auto issue = [&](int k, int s) {
     TileStage& st = sh.st[s];
 #pragma unroll
-    for (int j = 0; j < kWDma; ++j) dma16(c.wsrc[j] + k * 128, &st.w[(32 * wave + 8 * j) * 128]);
+    for (int j = 0; j < kWDma; ++j) dma16(c.wbase + k * 128 + c.woff[j], &st.w[(32 * wave + 8 * j) * 128]);
 #pragma unroll
     for (int j = 0; j < kADma; ++j) dma16(c.asrc[j] + k * 128, &st.a[(16 * wave + 8 * j) * 128]);
     dma4(c.ssrc + k * c.sstride, &st.sa[64 * wave]);
@@ -135,14 +137,30 @@ __device__ __forceinline__ void tile_body(const GemmParams& p, const TileCtx& c,
     else return 64 * wb + 16 * f + (lane & 15);
   };
 
-  auto compute = [&](int s, float s0, float s1) {
+  // The fragments a step starts with: its first row group and the four weight fragments.
+  // They are read from LDS right after the barrier, before the step's DMA issue, so that
+  // the issue overlaps their latency.
+  struct Head {
+    v8i wf[4];
+    v8i bf;
+    float sa;
+  };
+  auto load_head = [&](int s, Head& h) {
     if constexpr (NG > 0) {
       const TileStage& st = sh.st[s];
-      v8i wf[4];
+      h.bf = lds_frag(st.a, 64 * wa + (lane & 15), lane);
+      h.sa = st.sa[(4 * wa) * 64 + (lane & 15)];
 #pragma unroll
-      for (int f = 0; f < 4; ++f) wf[f] = lds_frag(st.w, wrow(f), lane);
-      v8i bf = lds_frag(st.a, 64 * wa + (lane & 15), lane);
-      float sa = st.sa[(4 * wa) * 64 + (lane & 15)];
+      for (int f = 0; f < 4; ++f) h.wf[f] = lds_frag(st.w, wrow(f), lane);
+    }
+  };
+
+  auto compute = [&](int s, const Head& h, float s0, float s1) {
+    if constexpr (NG > 0) {
+      const TileStage& st = sh.st[s];
+      const v8i (&wf)[4] = h.wf;
+      v8i bf = h.bf;
+      float sa = h.sa;
 #pragma unroll
       for (int g = 0; g < NG; ++g) {
         // the next row group's fragment is read from LDS while this group's MFMAs run
@@ -179,11 +197,14 @@ __device__ __forceinline__ void tile_body(const GemmParams& p, const TileCtx& c,
     // step k's loads are complete for this wave (only step k+1's may be in flight), and
     // after the barrier for every wave; every wave is also done with stage s_next (step k-1)
     ring_barrier<kLoadsPerStep>();
+    Head h;
+    load_head(s_cur, h);
+    __builtin_amdgcn_sched_barrier(0);
     issue(min(k + 2, KS - 1), s_next);   // past the last step: the last step again, never read
     __builtin_amdgcn_sched_barrier(0);
     const float s0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sw0_lane), k));
     const float s1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sw1_lane), k));
-    compute(s_cur, s0, s1);
+    compute(s_cur, h, s0, s1);
     s_cur = s_cur == kStages - 1 ? 0 : s_cur + 1;
     s_next = s_next == kStages - 1 ? 0 : s_next + 1;
   }
@@ -282,6 +303,7 @@ __global__ __launch_bounds__(kTileWaves * 64, 1) void gemm_tile_kernel(GemmParam
     c.rows = __builtin_amdgcn_readfirstlane(it.z);
     c.tile = __builtin_amdgcn_readfirstlane(v / ne);
 
+    c.wbase = G1 ? p.w13 : p.w2;
     // DMA j of this wave fills 8 tile rows, lane l writing row +l/8, physical chunk l%8
     // (activation rows past the item's end repeat its first row)
 #pragma unroll
@@ -291,7 +313,7 @@ __global__ __launch_bounds__(kTileWaves * 64, 1) void gemm_tile_kernel(GemmParam
       size_t grow;
       if constexpr (G1) grow = (size_t)e * 2 * kInter + (r < 128 ? c.tile * 128 + r : kInter + c.tile * 128 + r - 128);
       else grow = (size_t)e * kHidden + c.tile * kTileW + r;
-      c.wsrc[j] = (G1 ? p.w13 : p.w2) + grow * (G1 ? kHidden : kInter) + ch * 16;
+      c.woff[j] = (uint32_t)(grow * (G1 ? kHidden : kInter) + ch * 16);
     }
 #pragma unroll
     for (int j = 0; j < kADma; ++j) {
