@@ -11,12 +11,12 @@
 //          and requant_kernel turns each row's 128-column blocks into e4m3 with
 //          scale = max(amax/448, 1e-12) (kernel.py:131-135 uses 64-column blocks; this
 //          layer uses 128 so that GEMM2 sees one activation scale per K-step).
-//   GEMM2: slice = 32 hidden rows of W2[e] (224 slices); v = acc * routing weight
+//   GEMM2: slice = 64 hidden rows of W2[e] (112 slices); v = acc * routing weight
 //          (kernel.py:236-237); a token with one local assignment gets v written straight
 //          to its output row, the others park v in `partial` by flat slot for
 //          combine_kernel (the reference adds with fp32 atomics, kernel.py:246-250).
-// A wavefront streams its weight rows and the item's activation rows into a 4-deep
-// register ring (3 K-steps in flight). Every K-step is exactly one 128x128 scale block:
+// A wavefront streams its weight rows and the item's activation rows into a register ring
+// (the next K-step in flight while the current one computes). Every K-step is exactly one 128x128 scale block:
 // one v_mfma_f32_16x16x128_f8f6f4 per fragment pair, then acc += mfma * (s_act * s_w) in
 // fp32 (kernel.py:123-124 and :234).
 //
@@ -34,20 +34,30 @@ namespace {
 constexpr int kG1 = 1;
 constexpr int kG2 = 2;
 constexpr int kStreamWaves = 4;                      // wavefronts per work-group
-constexpr int kG1Slices = kInter / 16;               // 128 slices of 16 SwiGLU columns
-constexpr int kG2Slices = kHidden / 32;              // 224 slices of 32 hidden rows
 
+// Per kind: K-steps, weight fragments (16 rows each) per work unit, work units per item
+// and depth of the register ring.
+//   GEMM1: a unit is 16 SwiGLU columns = their 16 gate rows + 16 up rows (2 fragments).
+//   GEMM2: a unit is 64 hidden rows (4 fragments).
+// Both use a 2-slot ring (one K-step in flight per wavefront): the small register footprint
+// (92 and 132 VGPRs) keeps 5 and 3 wavefronts per SIMD resident, so at decode sizes every
+// unit has its own wavefront and the grid drains in one round (measured at T=64: GEMM1
+// 117 -> 109 us, GEMM2 64 -> 57 us against 4-slot rings and 32-row GEMM2 units).
 template <int KIND>
 struct StreamShape;
 template <>
 struct StreamShape<kG1> {
   static constexpr int kSteps = kHBlocks;   // K = 7168
-  static constexpr int kSlices = kG1Slices;
+  static constexpr int kFrags = 2;
+  static constexpr int kSlices = kInter / 16;
+  static constexpr int kRing = 2;
 };
 template <>
 struct StreamShape<kG2> {
   static constexpr int kSteps = kIBlocks;   // K = 2048
-  static constexpr int kSlices = kG2Slices;
+  static constexpr int kFrags = 4;
+  static constexpr int kSlices = kHidden / (16 * kFrags);
+  static constexpr int kRing = 2;
 };
 
 // One MFMA operand fragment: bytes [16g, 16g+16) and [64+16g, +16) of a 128-byte K block
@@ -58,9 +68,9 @@ __device__ __forceinline__ v8i load_frag(const uint8_t* p) {
   return join(lo, hi);
 }
 
-template <int NG>
+template <int NF, int NG>
 struct StreamStage {
-  v8i w[2];
+  v8i w[NF];
   v8i a[NG];
   float sa[NG];
 };
@@ -71,30 +81,31 @@ struct StreamStage {
 // holds no branches and the compiler's waits cover exactly the step being consumed.
 template <int KIND, int NG>
 __device__ __forceinline__ void stream_unit(const GemmParams& p, int e, int r0, int rows, int slice, int lane) {
-  constexpr int KS = StreamShape<KIND>::kSteps;
-  constexpr int NB = 4;
+  using S = StreamShape<KIND>;
+  constexpr int KS = S::kSteps;
+  constexpr int NF = S::kFrags;
+  constexpr int NB = S::kRing;
   static_assert(KS % NB == 0, "K-step count");
 
-  // weight fragments and their block-scale rows
-  const uint8_t* wf0;
-  const uint8_t* wf1;
-  const float* sw0;
-  const float* sw1;
+  // weight fragments and their block-scale rows; lane k of sw_lane[f] holds the scale of
+  // K-step k
+  const uint8_t* wf[NF];
+  float sw_lane[NF];
   if constexpr (KIND == kG1) {
     const int row = slice * 16 + (lane & 15);                 // gate row; up row = + I
-    wf0 = p.w13 + ((size_t)e * 2 * kInter + row) * kHidden + (lane >> 4) * 16;
-    wf1 = wf0 + (size_t)kInter * kHidden;
-    sw0 = p.w13_scale + ((size_t)e * 32 + slice / 8) * kHBlocks;
-    sw1 = p.w13_scale + ((size_t)e * 32 + kIBlocks + slice / 8) * kHBlocks;
+    wf[0] = p.w13 + ((size_t)e * 2 * kInter + row) * kHidden + (lane >> 4) * 16;
+    wf[1] = wf[0] + (size_t)kInter * kHidden;
+    sw_lane[0] = p.w13_scale[((size_t)e * 32 + slice / 8) * kHBlocks + (lane < KS ? lane : 0)];
+    sw_lane[1] = p.w13_scale[((size_t)e * 32 + kIBlocks + slice / 8) * kHBlocks + (lane < KS ? lane : 0)];
   } else {
-    const int row = slice * 32 + (lane & 15);                 // rows +0 and +16
-    wf0 = p.w2 + ((size_t)e * kHidden + row) * kInter + (lane >> 4) * 16;
-    wf1 = wf0 + (size_t)16 * kInter;
-    sw0 = p.w2_scale + ((size_t)e * kHBlocks + slice / 4) * kIBlocks;
-    sw1 = sw0;
+    const int row0 = slice * 16 * NF;                         // fragments at row0 + 16f
+#pragma unroll
+    for (int f = 0; f < NF; ++f)
+      wf[f] = p.w2 + ((size_t)e * kHidden + row0 + 16 * f + (lane & 15)) * kInter + (lane >> 4) * 16;
+    const float sw = p.w2_scale[((size_t)e * kHBlocks + row0 / 128) * kIBlocks + (lane < KS ? lane : 0)];
+#pragma unroll
+    for (int f = 0; f < NF; ++f) sw_lane[f] = sw;
   }
-  const float sw0_lane = sw0[lane < KS ? lane : 0];
-  const float sw1_lane = sw1[lane < KS ? lane : 0];
 
   // activation rows of this lane's column in each 16-row group (rows past the item's end
   // read its first row; their results are never stored)
@@ -115,10 +126,10 @@ __device__ __forceinline__ void stream_unit(const GemmParams& p, int e, int r0, 
   }
   const size_t sa_stride = (KIND == kG1) ? (size_t)p.T : 1;
 
-  StreamStage<NG> ring[NB];
-  auto issue = [&](int k, StreamStage<NG>& st) {
-    st.w[0] = load_frag(wf0 + k * 128);
-    st.w[1] = load_frag(wf1 + k * 128);
+  StreamStage<NF, NG> ring[NB];
+  auto issue = [&](int k, StreamStage<NF, NG>& st) {
+#pragma unroll
+    for (int f = 0; f < NF; ++f) st.w[f] = load_frag(wf[f] + k * 128);
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
       st.a[g] = load_frag(ap[g] + k * 128);
@@ -128,12 +139,11 @@ __device__ __forceinline__ void stream_unit(const GemmParams& p, int e, int r0, 
 #pragma unroll
   for (int s = 0; s < NB - 1; ++s) issue(s, ring[s]);
 
-  v4f acc0[NG], acc1[NG];
+  v4f acc[NF][NG];
 #pragma unroll
-  for (int g = 0; g < NG; ++g) {
-    acc0[g] = v4f{0.f, 0.f, 0.f, 0.f};
-    acc1[g] = v4f{0.f, 0.f, 0.f, 0.f};
-  }
+  for (int f = 0; f < NF; ++f)
+#pragma unroll
+    for (int g = 0; g < NG; ++g) acc[f][g] = v4f{0.f, 0.f, 0.f, 0.f};
   const v4f zero = {0.f, 0.f, 0.f, 0.f};
 #pragma nounroll
   for (int k0 = 0; k0 < KS; k0 += NB) {
@@ -144,16 +154,17 @@ __device__ __forceinline__ void stream_unit(const GemmParams& p, int e, int r0, 
       // keep each step's loads ahead of its math (the scheduler would otherwise pull later
       // steps' MFMAs above these loads and shrink the ring to one step in flight)
       __builtin_amdgcn_sched_barrier(0);
-      const StreamStage<NG>& st = ring[u];
-      const float s0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sw0_lane), k));
-      const float s1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sw1_lane), k));
+      const StreamStage<NF, NG>& st = ring[u];
+      float sc[NF];
 #pragma unroll
-      for (int g = 0; g < NG; ++g) {
-        const v4f d0 = mfma16x16x128_fp8(st.w[0], st.a[g], zero);
-        const v4f d1 = mfma16x16x128_fp8(st.w[1], st.a[g], zero);
-        acc0[g] += d0 * (st.sa[g] * s0);
-        acc1[g] += d1 * (st.sa[g] * s1);
-      }
+      for (int f = 0; f < NF; ++f) sc[f] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sw_lane[f]), k));
+#pragma unroll
+      for (int g = 0; g < NG; ++g)
+#pragma unroll
+        for (int f = 0; f < NF; ++f) {
+          const v4f d = mfma16x16x128_fp8(st.w[f], st.a[g], zero);
+          acc[f][g] += d * (st.sa[g] * sc[f]);
+        }
       __builtin_amdgcn_sched_barrier(0);
     }
   }
@@ -168,7 +179,7 @@ __device__ __forceinline__ void stream_unit(const GemmParams& p, int e, int r0, 
       v4f c;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float x1 = acc0[g][i], x2 = acc1[g][i];
+        const float x1 = acc[0][g][i], x2 = acc[1][g][i];
         c[i] = (x2 / (1.0f + __expf(-x2))) * x1;
       }
       *reinterpret_cast<v4f*>(p.swiglu + (size_t)pr * kInter + slice * 16 + 4 * (lane >> 4)) = c;
@@ -178,9 +189,9 @@ __device__ __forceinline__ void stream_unit(const GemmParams& p, int e, int r0, 
       const bool direct = p.token_nlocal[t] == 1;
       const size_t slot = (size_t)p.sorted_slot[pr];
 #pragma unroll
-      for (int f = 0; f < 2; ++f) {
-        const v4f v = (f == 0 ? acc0[g] : acc1[g]) * wt;
-        const int h = slice * 32 + f * 16 + 4 * (lane >> 4);
+      for (int f = 0; f < NF; ++f) {
+        const v4f v = acc[f][g] * wt;
+        const int h = slice * 16 * NF + f * 16 + 4 * (lane >> 4);
         if (direct) {
           if (p.out_dtype == MOE_FP8_OUT_BF16)
             *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(p.out) + (size_t)t * kHidden + h) =

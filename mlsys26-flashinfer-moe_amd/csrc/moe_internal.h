@@ -30,9 +30,10 @@ constexpr int kBlock = MOE_FP8_BLOCK;          // 128
 constexpr int kHBlocks = MOE_FP8_H_BLOCKS;     // 56
 constexpr int kIBlocks = MOE_FP8_I_BLOCKS;     // 16
 
-// Routing: one wavefront per token, 16 tokens per work-group of 1024 threads.
+// Routing: 16 lanes per token, 16 tokens per work-group of 4 wavefronts; the one-work-group
+// dispatch of small batches and the scan use 1024 threads.
 constexpr int kRouteTokensPerBlock = 16;
-constexpr int kRouteThreads = 64 * kRouteTokensPerBlock;
+constexpr int kRouteThreads = 1024;
 // Up to this many tokens routing and dispatch run in a single work-group (one launch).
 constexpr int kSinglePassTokens = 256;
 

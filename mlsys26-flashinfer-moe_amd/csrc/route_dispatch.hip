@@ -82,20 +82,31 @@ __device__ __forceinline__ int group_beats(float gs, int g) {
   return (pv > gs || (pv == gs && pg < g)) ? 1 : 0;
 }
 
+// Token routed by this lane's 16-lane row when the wavefront routes tokens t0 .. t0+3.
+__device__ __forceinline__ int route_row(int t0, int T) {
+  return min(t0 + (lane_id() >> 4), T - 1);   // rows past the end recompute the last token
+}
+__device__ __forceinline__ void load_logits(const RouteParams& p, int t0, float4 (&lg)[4]) {
+  const float4* lp = reinterpret_cast<const float4*>(p.logits + (size_t)route_row(t0, p.T) * kExpertsGlobal +
+                                                     16 * (lane_id() & 15));
+#pragma unroll
+  for (int i = 0; i < 4; ++i) lg[i] = lp[i];
+}
 // Routing of 4 tokens by one wavefront (kernel.py:428-542). Token q = lane/16 of the
 // wavefront is t0 + q; lane r = lane%16 of its row holds experts 16r..16r+15, so group g
-// (32 experts) is lanes 2g, 2g+1. Returns in lanes r < 8 the expert of top-k slot r (in
-// selection order) and its weight; other lanes return id -1.
-__device__ __forceinline__ int route_wave(const RouteParams& p, const float* s_bias, int t0, float& w_out) {
+// (32 experts) is lanes 2g, 2g+1. The lane's 16 logits come in `lg` (loaded by the caller
+// before the bias staging barrier, so that the two loads overlap). Returns in lanes r < 8
+// the expert of top-k slot r (in selection order) and its weight; other lanes return -1.
+__device__ __forceinline__ int route_wave(const RouteParams& p, const float* s_bias, int t0, const float4 (&lg)[4],
+                                          float& w_out) {
   const int lane = lane_id();
   const int r = lane & 15;
-  const int t = min(t0 + (lane >> 4), p.T - 1);   // rows past the end recompute the last token
-  const float4* lp = reinterpret_cast<const float4*>(p.logits + (size_t)t * kExpertsGlobal + 16 * r);
+  const int t = route_row(t0, p.T);
   const float4* bp = reinterpret_cast<const float4*>(s_bias + 16 * r);
   float s[16], b[16];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const float4 x = lp[i], c = bp[i];
+    const float4 x = lg[i], c = bp[i];
     const float xs[4] = {x.x, x.y, x.z, x.w}, cs[4] = {c.x, c.y, c.z, c.w};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -281,11 +292,13 @@ __global__ __launch_bounds__(kRouteWaves * 64) void route_kernel(RouteParams p) 
   const int tw = blockIdx.x * kRouteTokensPerBlock + wave * 4;   // first token of the wavefront
   const int t = tw + (lane >> 4);                                 // token of this lane's row
   const bool slot_lane = t < p.T && r < kTopK;                    // lane holds slot t*8 + r
+  float4 lg[4];
+  if (!p.skip_routing) load_logits(p, tw, lg);
   stage_bias(p, s_bias);
   int id = -1;
   float w = 0.f;
   if (!p.skip_routing) {
-    id = route_wave(p, s_bias, tw, w);
+    id = route_wave(p, s_bias, tw, lg, w);
     if (slot_lane) {
       p.topk_ids[t * kTopK + r] = id;
       p.topk_w[t * kTopK + r] = w;
