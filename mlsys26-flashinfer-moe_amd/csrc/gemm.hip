@@ -39,10 +39,11 @@ constexpr int kStreamWaves = 4;                      // wavefronts per work-grou
 // and depth of the register ring.
 //   GEMM1: a unit is 16 SwiGLU columns = their 16 gate rows + 16 up rows (2 fragments).
 //   GEMM2: a unit is 64 hidden rows (4 fragments).
-// Both use a 2-slot ring (one K-step in flight per wavefront): the small register footprint
-// (92 and 132 VGPRs) keeps 5 and 3 wavefronts per SIMD resident, so at decode sizes every
-// unit has its own wavefront and the grid drains in one round (measured at T=64: GEMM1
-// 117 -> 109 us, GEMM2 64 -> 57 us against 4-slot rings and 32-row GEMM2 units).
+// GEMM1 uses a 3-slot ring (two K-steps in flight per wavefront, 114 VGPRs, 4 wavefronts
+// per SIMD), GEMM2 a 2-slot ring (132 VGPRs, 3 per SIMD): small register footprints keep
+// enough wavefronts resident that at decode sizes every unit has its own wavefront and the
+// grid drains in one round (measured at T=64: GEMM1 117 -> 109 us, GEMM2 64 -> 57 us
+// against 4-slot rings and 32-row GEMM2 units).
 template <int KIND>
 struct StreamShape;
 template <>
@@ -50,7 +51,7 @@ struct StreamShape<kG1> {
   static constexpr int kSteps = kHBlocks;   // K = 7168
   static constexpr int kFrags = 2;
   static constexpr int kSlices = kInter / 16;
-  static constexpr int kRing = 2;
+  static constexpr int kRing = 3;
 };
 template <>
 struct StreamShape<kG2> {
@@ -85,7 +86,7 @@ __device__ __forceinline__ void stream_unit(const GemmParams& p, int e, int r0, 
   constexpr int KS = S::kSteps;
   constexpr int NF = S::kFrags;
   constexpr int NB = S::kRing;
-  static_assert(KS % NB == 0, "K-step count");
+  constexpr int KMAIN = KS - KS % NB;   // steps of the ring-unrolled main loop
 
   // weight fragments and their block-scale rows; lane k of sw_lane[f] holds the scale of
   // K-step k
@@ -145,29 +146,32 @@ __device__ __forceinline__ void stream_unit(const GemmParams& p, int e, int r0, 
 #pragma unroll
     for (int g = 0; g < NG; ++g) acc[f][g] = v4f{0.f, 0.f, 0.f, 0.f};
   const v4f zero = {0.f, 0.f, 0.f, 0.f};
+  // step k: refill the slot step k-1 used with step k+NB-1, then consume slot u = k % NB
+  auto step = [&](int k, int u) {
+    issue(min(k + NB - 1, KS - 1), ring[(u + NB - 1) % NB]);
+    // keep each step's loads ahead of its math (the scheduler would otherwise pull later
+    // steps' MFMAs above these loads and shrink the ring to one step in flight)
+    __builtin_amdgcn_sched_barrier(0);
+    const StreamStage<NF, NG>& st = ring[u];
+    float sc[NF];
+#pragma unroll
+    for (int f = 0; f < NF; ++f) sc[f] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sw_lane[f]), k));
+#pragma unroll
+    for (int g = 0; g < NG; ++g)
+#pragma unroll
+      for (int f = 0; f < NF; ++f) {
+        const v4f d = mfma16x16x128_fp8(st.w[f], st.a[g], zero);
+        acc[f][g] += d * (st.sa[g] * sc[f]);
+      }
+    __builtin_amdgcn_sched_barrier(0);
+  };
 #pragma nounroll
-  for (int k0 = 0; k0 < KS; k0 += NB) {
+  for (int k0 = 0; k0 < KMAIN; k0 += NB) {
 #pragma unroll
-    for (int u = 0; u < NB; ++u) {
-      const int k = k0 + u;
-      issue(min(k + NB - 1, KS - 1), ring[(u + NB - 1) % NB]);
-      // keep each step's loads ahead of its math (the scheduler would otherwise pull later
-      // steps' MFMAs above these loads and shrink the ring to one step in flight)
-      __builtin_amdgcn_sched_barrier(0);
-      const StreamStage<NF, NG>& st = ring[u];
-      float sc[NF];
-#pragma unroll
-      for (int f = 0; f < NF; ++f) sc[f] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sw_lane[f]), k));
-#pragma unroll
-      for (int g = 0; g < NG; ++g)
-#pragma unroll
-        for (int f = 0; f < NF; ++f) {
-          const v4f d = mfma16x16x128_fp8(st.w[f], st.a[g], zero);
-          acc[f][g] += d * (st.sa[g] * sc[f]);
-        }
-      __builtin_amdgcn_sched_barrier(0);
-    }
+    for (int u = 0; u < NB; ++u) step(k0 + u, u);
   }
+#pragma unroll
+  for (int u = 0; u < KS - KMAIN; ++u) step(KMAIN + u, u);
 
   // lane: column (lane & 15) of each row group, fragment rows 4*(lane>>4) + i
 #pragma unroll
@@ -231,11 +235,13 @@ __global__ __launch_bounds__(kStreamWaves * 64) void gemm_stream_kernel(GemmPara
 // and q = e4m3(c / scale) (kernel.py:131-135 with 128-column blocks). One work-group of 256
 // threads per row; 16 threads (8 columns each) per block.
 __global__ __launch_bounds__(256) void requant_kernel(GemmParams p) {
-  const int n = p.counters[kCtrAssign];
+  const int nmax = p.T * kTopK;   // rows of the SwiGLU buffer
   const int tid = threadIdx.x;
-  for (int r = blockIdx.x; r < n; r += gridDim.x) {
+  for (int r = blockIdx.x; r < nmax; r += gridDim.x) {
+    // the row is loaded together with the number of rows in use (no dependent round trip)
     const v4f* src = reinterpret_cast<const v4f*>(p.swiglu + (size_t)r * kInter) + 2 * tid;
     const v4f a = src[0], b = src[1];
+    if (r >= p.counters[kCtrAssign]) break;
     float amax = fmaxf(fmaxf(fmaxf(fabsf(a[0]), fabsf(a[1])), fmaxf(fabsf(a[2]), fabsf(a[3]))),
                        fmaxf(fmaxf(fabsf(b[0]), fabsf(b[1])), fmaxf(fabsf(b[2]), fabsf(b[3]))));
 #pragma unroll
@@ -262,8 +268,9 @@ __global__ __launch_bounds__(256) void combine_kernel(GemmParams p) {
   const int items = p.T * kCombineChunks;
   for (int it = blockIdx.x * 4 + (threadIdx.x >> 6); it < items; it += nwaves) {
     const int t = it / kCombineChunks, ch = it - t * kCombineChunks;
-    if (__builtin_amdgcn_readfirstlane(p.token_nlocal[t]) == 1) continue;
+    // the local count and the top-k ids are loaded together (no dependent round trip)
     const int le = lane < kTopK ? p.topk_ids[t * kTopK + lane] - p.offset : -1;
+    if (__builtin_amdgcn_readfirstlane(p.token_nlocal[t]) == 1) continue;
     const uint32_t mask = (uint32_t)__ballot(le >= 0 && le < kExpertsLocal);
     const int v0 = ch * kPerLane * 64 + lane;
     const v4f* rows = reinterpret_cast<const v4f*>(p.partial + (size_t)t * kTopK * kHidden) + v0;
@@ -339,7 +346,7 @@ hipError_t launch_gemm1(const GemmParams& p, int rows_per_item, hipStream_t s) {
 
 hipError_t launch_requant(const GemmParams& p, int rows_per_item, hipStream_t s) {
   if (rows_per_item > 32) return hipSuccess;   // the tile GEMM1 requantises in its epilogue
-  int grid = p.max_items * rows_per_item;      // >= the number of SwiGLU rows
+  int grid = p.T * kTopK;                      // rows of the SwiGLU buffer
   if (grid > num_cus() * 8) grid = num_cus() * 8;
   if (grid > 0) hipLaunchKernelGGL(requant_kernel, dim3(grid), dim3(256), 0, s, p);
   return hipGetLastError();

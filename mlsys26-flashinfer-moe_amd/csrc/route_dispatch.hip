@@ -335,6 +335,24 @@ __global__ __launch_bounds__(kRouteThreads) void dispatch_small_kernel(RoutePara
 
   const int tid = threadIdx.x;
   const int nslots = p.T * kTopK;
+  if (nslots <= kRouteThreads) {
+    // One slot per thread, kept in registers: the 8 slots of token tid/8 are 8 consecutive
+    // lanes, so one ballot gives every token's local count.
+    const int le = tid < nslots ? local_of(p.topk_ids[tid], p.offset) : -1;
+    const float w = tid < nslots ? p.topk_w[tid] : 0.f;
+    const uint64_t m = __ballot(le >= 0);
+    if ((tid & 7) == 0 && tid < nslots) p.token_nlocal[tid >> 3] = __popcll((m >> (lane_id() & 56)) & 0xFFull);
+    const int r = block_rank(le, kRouteThreads / 64, s_wcnt, s_cnt);
+    if (tid < kExpertsLocal) finish_counts(p, tid, s_cnt[tid], s_start);
+    __syncthreads();
+    if (le >= 0) {
+      const int pos = s_start[le] + r;
+      p.sorted_token[pos] = tid >> 3;
+      p.sorted_weight[pos] = w;
+      p.sorted_slot[pos] = tid;
+    }
+    return;
+  }
   for (int slot = tid; slot < nslots; slot += kRouteThreads) {
     s_le[slot] = local_of(p.topk_ids[slot], p.offset);
     s_w[slot] = p.topk_w[slot];
