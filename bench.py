@@ -19,7 +19,9 @@ The JSON line also carries:
   cpu_baseline  the numpy oracle (fp32 dequantise-and-matmul) on the same workload, timed on
                 the host cores;
   workloads     the same figures for the other four workloads (T=16, 1024 with offset 64,
-                8192, 4096 skewed).
+                8192, 4096 skewed), each with the upstream activation quantiser
+                (quantize_hidden: bf16 [T,7168] -> e4m3fn + scales [56,T]) timed beside the
+                layer; its bytes are T * 21,728 (14,336 read, 7,168 + 224 written).
 """
 from __future__ import annotations
 
@@ -138,6 +140,28 @@ def bench_workload(pkg, inputs, name, weight_sets, steps, warmup):
     torch.cuda.synchronize()
     stage_ms = [sum(evs[i][j].elapsed_time(evs[i][j + 1]) for i in range(steps)) / steps for j in range(3)]
 
+    # the step before the layer: bf16 hidden states -> e4m3fn + 1x128 scales; three buffer
+    # sets rotate so that large T streams from HBM
+    qsets = []
+    for i in range(3):
+        x = torch.randn((T, 7168), device=dev, generator=torch.Generator(device=dev).manual_seed(40 + i))
+        qsets.append((x.to(torch.bfloat16), torch.empty((T, 7168), dtype=torch.float8_e4m3fn, device=dev),
+                      torch.empty((56, T), dtype=torch.float32, device=dev)))
+    for i in range(3):
+        pkg.quantize_hidden(qsets[i][0], qsets[i][1], qsets[i][2])
+    q0, q1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    q0.record(stream)
+    for i in range(steps):
+        x, qo, so = qsets[i % 3]
+        _lib.check(lib.moe_fp8_quantize_hidden(x.data_ptr(), _lib.HIDDEN_BF16, T, qo.data_ptr(), so.data_ptr(), sptr),
+                   "moe_fp8_quantize_hidden")
+    q1.record(stream)
+    torch.cuda.synchronize()
+    q_us = q0.elapsed_time(q1) / steps * 1e3
+    q_bytes = T * (7168 * 2 + 7168 + 56 * 4)
+    del qsets
+
     f = workload_figures(T, n, e_touched, u)
     us = ms_per_step * 1e3
     res = dict(T=T, offset=wl.local_expert_offset, assignments=n, experts_touched=e_touched,
@@ -149,6 +173,9 @@ def bench_workload(pkg, inputs, name, weight_sets, steps, warmup):
     res["rows_per_item"] = int(ws.layout.rows_per_item)
     res["hbm_roofline_frac"] = round(res["hbm_gbs"] / HBM_PEAK_GBS, 4)
     res["mfma_roofline_frac"] = round(res["tflops"] / FP8_PEAK_TFLOPS, 4)
+    q_gbs = q_bytes / (q_us * 1e-6) / 1e9
+    res["quantize_hidden"] = dict(us=round(q_us, 2), bytes=q_bytes, gbs=round(q_gbs, 1),
+                                  hbm_roofline_frac=round(q_gbs / HBM_PEAK_GBS, 4))
     return res, f, stage_ms, kw
 
 

@@ -47,6 +47,11 @@ extern "C" {
 #define MOE_FP8_BIAS_BF16  1
 #define MOE_FP8_BIAS_F16   2
 
+/* hidden_dtype of moe_fp8_quantize_hidden: the element type of the unquantised states. */
+#define MOE_FP8_HIDDEN_F32   0
+#define MOE_FP8_HIDDEN_BF16  1
+#define MOE_FP8_HIDDEN_F16   2
+
 /* output element type. The reference copies its fp32 accumulator into the caller's
  * tensor (kernel.py:729); bf16 is the contract type, fp32 is offered so that an
  * fp32 destination receives the unrounded sums as it would from the reference. */
@@ -62,6 +67,7 @@ extern "C" {
 #define MOE_FP8_EINVAL_OUT_DTYPE   -5
 #define MOE_FP8_ELAUNCH            -6  /* a HIP launch failed (hipGetLastError) */
 #define MOE_FP8_EDEVICE            -7  /* current device is not gfx950 */
+#define MOE_FP8_EINVAL_HIDDEN_DTYPE -8 /* hidden_dtype of moe_fp8_quantize_hidden unknown */
 
 /* Largest num_tokens accepted: keeps every flat index (T*8*7168) inside int64 and
  * the per-token slot index inside int32. */
@@ -177,6 +183,15 @@ int moe_fp8_gemm1(const moe_fp8_args* args, void* workspace, size_t workspace_by
  * Replaces moe_gemm2_kernel and the finalize copy (kernel.py:695-729, 153-250). */
 int moe_fp8_gemm2_combine(const moe_fp8_args* args, void* workspace, size_t workspace_bytes,
                           hipStream_t stream);
+
+/* The step before the layer: quantises hidden states [T, 7168] (element type hidden_dtype)
+ * to the layer's activation contract, e4m3fn hidden_fp8 [T, 7168] and fp32 hidden_scale
+ * [56, T] (token-minor), per token and 128-column block: scale = max(amax / 448, 1e-12),
+ * hidden_fp8 = e4m3(x / scale) rounded to nearest even. No workspace. num_tokens == 0 is
+ * a no-op. The reference takes these tensors already quantised (kernel.py:600-603); the
+ * formula is its own in-path requantisation (kernel.py:131-135) with 128 columns. */
+int moe_fp8_quantize_hidden(const void* hidden, int32_t hidden_dtype, int32_t num_tokens,
+                            void* hidden_fp8, float* hidden_scale, hipStream_t stream);
 
 /* Text for a return code. */
 const char* moe_fp8_strerror(int code);

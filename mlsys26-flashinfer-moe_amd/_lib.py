@@ -27,6 +27,7 @@ G1_BLOCKS = 2 * INTER // BLOCK
 MAX_TOKENS = 1 << 20
 
 BIAS_F32, BIAS_BF16, BIAS_F16 = 0, 1, 2
+HIDDEN_F32, HIDDEN_BF16, HIDDEN_F16 = 0, 1, 2
 OUT_BF16, OUT_F32 = 0, 1
 
 OK = 0
@@ -37,6 +38,7 @@ EINVAL_BIAS_DTYPE = -4
 EINVAL_OUT_DTYPE = -5
 ELAUNCH = -6
 EDEVICE = -7
+EINVAL_HIDDEN_DTYPE = -8
 
 EXPORTED_SYMBOLS = (
     "moe_fp8_workspace_bytes",
@@ -46,6 +48,7 @@ EXPORTED_SYMBOLS = (
     "moe_fp8_route_dispatch",
     "moe_fp8_gemm1",
     "moe_fp8_gemm2_combine",
+    "moe_fp8_quantize_hidden",
     "moe_fp8_strerror",
     "moe_fp8_version",
 )
@@ -134,6 +137,8 @@ def load() -> ctypes.CDLL:
         lib.moe_fp8_gemm1.restype = ctypes.c_int
         lib.moe_fp8_gemm2_combine.argtypes = [args_p, vp, sz, vp]
         lib.moe_fp8_gemm2_combine.restype = ctypes.c_int
+        lib.moe_fp8_quantize_hidden.argtypes = [vp, i32, i32, vp, vp, vp]
+        lib.moe_fp8_quantize_hidden.restype = ctypes.c_int
         lib.moe_fp8_strerror.argtypes = [ctypes.c_int]
         lib.moe_fp8_strerror.restype = ctypes.c_char_p
         lib.moe_fp8_version.argtypes = []

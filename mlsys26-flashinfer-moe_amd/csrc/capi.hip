@@ -218,6 +218,20 @@ int moe_fp8_run(const moe_fp8_args* args, void* workspace, size_t workspace_byte
   return MOE_FP8_OK;
 }
 
+int moe_fp8_quantize_hidden(const void* hidden, int32_t hidden_dtype, int32_t num_tokens, void* hidden_fp8,
+                            float* hidden_scale, hipStream_t stream) {
+  if (num_tokens < 0 || num_tokens > MOE_FP8_MAX_TOKENS) return MOE_FP8_EINVAL_TOKENS;
+  if (num_tokens == 0) return MOE_FP8_OK;
+  if (!hidden || !hidden_fp8 || !hidden_scale) return MOE_FP8_EINVAL_POINTER;
+  if (hidden_dtype < MOE_FP8_HIDDEN_F32 || hidden_dtype > MOE_FP8_HIDDEN_F16) return MOE_FP8_EINVAL_HIDDEN_DTYPE;
+  const int rc = check_device();
+  if (rc != MOE_FP8_OK) return rc;
+  return launch_quantize_hidden(hidden, hidden_dtype, num_tokens, static_cast<uint8_t*>(hidden_fp8), hidden_scale,
+                                stream) == hipSuccess
+             ? MOE_FP8_OK
+             : MOE_FP8_ELAUNCH;
+}
+
 const char* moe_fp8_strerror(int code) {
   switch (code) {
     case MOE_FP8_OK: return "success";
@@ -228,6 +242,7 @@ const char* moe_fp8_strerror(int code) {
     case MOE_FP8_EINVAL_OUT_DTYPE: return "output_dtype must be MOE_FP8_OUT_BF16 or MOE_FP8_OUT_F32";
     case MOE_FP8_ELAUNCH: return "a HIP kernel launch failed";
     case MOE_FP8_EDEVICE: return "the current HIP device is not a gfx950 (MI355X) GPU";
+    case MOE_FP8_EINVAL_HIDDEN_DTYPE: return "hidden_dtype must be MOE_FP8_HIDDEN_F32, _BF16 or _F16";
     default: return "unknown error code";
   }
 }

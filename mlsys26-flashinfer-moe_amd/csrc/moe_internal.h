@@ -109,6 +109,7 @@ hipError_t launch_requant(const GemmParams& p, int rows_per_item, hipStream_t s)
 hipError_t launch_gemm2(const GemmParams& p, int rows_per_item, hipStream_t s);
 hipError_t launch_combine(const GemmParams& p, hipStream_t s);
 hipError_t launch_gemm1_tile(const GemmParams& p, hipStream_t s);
+hipError_t launch_quantize_hidden(const void* x, int dtype, int T, uint8_t* q, float* scale, hipStream_t s);
 hipError_t launch_gemm2_tile(const GemmParams& p, hipStream_t s);
 
 }  // namespace moe

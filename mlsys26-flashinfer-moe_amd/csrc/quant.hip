@@ -1,0 +1,92 @@
+// Upstream activation quantiser: hidden states [T, 7168] (bf16, fp16 or fp32) -> OCP e4m3fn
+// [T, 7168] plus per-token 1x128 block scales [56, T] (token-minor), the tensors run()
+// takes (kernel.py:600-603). Per token and 128-column block:
+//   scale = max(amax / 448, 1e-12),  q = e4m3(x / scale), round to nearest even,
+// the reference's own in-path quantisation (kernel.py:131-135) with 128 columns.
+//
+// HBM-bound: 2 or 4 bytes read and 1 byte written per element, plus 4 bytes of scale per
+// block. A work-group of 256 threads takes one 128-column block of 16 consecutive tokens:
+// 16 lanes per token row, 8 elements per lane (one 16- or 32-byte load, one 8-byte store),
+// the block's amax reduced over its 16 lanes, and the 16 scales written as one 64-byte
+// segment of the token-minor scale array. Consecutive work-groups take neighbouring blocks
+// of the same rows.
+#include <hip/hip_fp16.h>
+
+#include "moe_internal.h"
+#include "moe_device.h"
+
+namespace moe {
+
+namespace {
+
+constexpr int kQTokens = 16;   // tokens per work-group
+
+template <int DT>
+__device__ __forceinline__ void load8(const void* x, size_t e, float (&v)[8]) {
+  if constexpr (DT == MOE_FP8_HIDDEN_F32) {
+    const v4f a = *reinterpret_cast<const v4f*>(reinterpret_cast<const float*>(x) + e);
+    const v4f b = *reinterpret_cast<const v4f*>(reinterpret_cast<const float*>(x) + e + 4);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[i] = a[i];
+      v[4 + i] = b[i];
+    }
+  } else {
+    const v4i r = *reinterpret_cast<const v4i*>(reinterpret_cast<const uint16_t*>(x) + e);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t w = (uint32_t)r[i];
+      if constexpr (DT == MOE_FP8_HIDDEN_BF16) {
+        v[2 * i] = __uint_as_float(w << 16);
+        v[2 * i + 1] = __uint_as_float(w & 0xFFFF0000u);
+      } else {
+        v[2 * i] = __half2float(__ushort_as_half((unsigned short)(w & 0xFFFF)));
+        v[2 * i + 1] = __half2float(__ushort_as_half((unsigned short)(w >> 16)));
+      }
+    }
+  }
+}
+
+template <int DT>
+__global__ __launch_bounds__(256) void quantize_hidden_kernel(const void* x, int T, uint8_t* q, float* scale) {
+  const int b = blockIdx.x % kHBlocks;
+  const int t = (blockIdx.x / kHBlocks) * kQTokens + (threadIdx.x >> 4);
+  const int l = threadIdx.x & 15;
+  // rows past T repeat the last row, so every 16-lane group reduces real data
+  const size_t e = (size_t)(t < T ? t : T - 1) * kHidden + b * kBlock + l * 8;
+  float v[8];
+  load8<DT>(x, e, v);
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+#pragma unroll
+  for (int m = 1; m < 16; m <<= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 16));
+  const float s = fmaxf(amax / 448.0f, 1e-12f);
+  if (t < T) {
+    uint2 packed;
+    packed.x = pack_fp8x4(v[0] / s, v[1] / s, v[2] / s, v[3] / s);
+    packed.y = pack_fp8x4(v[4] / s, v[5] / s, v[6] / s, v[7] / s);
+    *reinterpret_cast<uint2*>(q + e) = packed;
+    if (l == 0) scale[(size_t)b * T + t] = s;
+  }
+}
+
+}  // namespace
+
+hipError_t launch_quantize_hidden(const void* x, int dtype, int T, uint8_t* q, float* scale, hipStream_t s) {
+  const int grid = ((T + kQTokens - 1) / kQTokens) * kHBlocks;
+  switch (dtype) {
+    case MOE_FP8_HIDDEN_F32:
+      hipLaunchKernelGGL(quantize_hidden_kernel<MOE_FP8_HIDDEN_F32>, dim3(grid), dim3(256), 0, s, x, T, q, scale);
+      break;
+    case MOE_FP8_HIDDEN_BF16:
+      hipLaunchKernelGGL(quantize_hidden_kernel<MOE_FP8_HIDDEN_BF16>, dim3(grid), dim3(256), 0, s, x, T, q, scale);
+      break;
+    default:
+      hipLaunchKernelGGL(quantize_hidden_kernel<MOE_FP8_HIDDEN_F16>, dim3(grid), dim3(256), 0, s, x, T, q, scale);
+      break;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace moe

@@ -13,7 +13,8 @@ import torch
 
 from . import _lib
 from ._lib import (BIAS_BF16, BIAS_F16, BIAS_F32, EXPERTS_GLOBAL, EXPERTS_LOCAL, G1_BLOCKS,
-                   H_BLOCKS, HIDDEN, I_BLOCKS, INTER, OUT_BF16, OUT_F32)
+                   H_BLOCKS, HIDDEN, HIDDEN_BF16, HIDDEN_F16, HIDDEN_F32, I_BLOCKS, INTER, OUT_BF16,
+                   OUT_F32)
 
 _BIAS_CODES = {torch.float32: BIAS_F32, torch.bfloat16: BIAS_BF16, torch.float16: BIAS_F16}
 
@@ -187,3 +188,41 @@ def run(
     if not direct:
         output.copy_(dst)
     return None
+
+
+_HIDDEN_CODES = {torch.float32: HIDDEN_F32, torch.bfloat16: HIDDEN_BF16, torch.float16: HIDDEN_F16}
+
+
+@torch.no_grad()
+def quantize_hidden(hidden: torch.Tensor, out: torch.Tensor | None = None,
+                    out_scale: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """The step before `run`: hidden states [T, 7168] (bf16, fp16 or fp32) to the layer's
+    activation contract (kernel.py:600-603): e4m3fn [T, 7168] and fp32 scales [56, T],
+    per token and 128-column block scale = max(amax / 448, 1e-12), q = e4m3(x / scale)
+    rounded to nearest even (the reference's in-path requantisation, kernel.py:131-135).
+
+    Returns (hidden_states, hidden_states_scale), written into `out` / `out_scale` when
+    given (contiguous tensors of those shapes and dtypes on the input's GPU).
+    """
+    assert hidden.dtype in _HIDDEN_CODES, "hidden must be float32, bfloat16 or float16"
+    assert hidden.dim() == 2 and hidden.shape[1] == HIDDEN, "hidden must be [T, 7168]"
+    device = _ensure_cuda(hidden, out, out_scale)
+    x = _check_cuda_and_move(hidden, device).contiguous()
+    T = int(x.shape[0])
+    if out is None:
+        out = torch.empty((T, HIDDEN), dtype=torch.float8_e4m3fn, device=x.device)
+    if out_scale is None:
+        out_scale = torch.empty((H_BLOCKS, T), dtype=torch.float32, device=x.device)
+    assert out.dtype == torch.float8_e4m3fn and tuple(out.shape) == (T, HIDDEN), "out must be float8_e4m3fn [T, 7168]"
+    assert out_scale.dtype == torch.float32 and tuple(out_scale.shape) == (H_BLOCKS, T), \
+        "out_scale must be float32 [56, T]"
+    for t in (out, out_scale):
+        if not (t.is_cuda and t.device == x.device and t.is_contiguous()):
+            raise RuntimeError("out and out_scale must be contiguous tensors on the input's device")
+    if T == 0:
+        return out, out_scale
+    with torch.cuda.device(x.device):
+        stream = torch.cuda.current_stream(x.device).cuda_stream
+        _lib.check(_lib.load().moe_fp8_quantize_hidden(x.data_ptr(), _HIDDEN_CODES[x.dtype], T, out.data_ptr(),
+                                                       out_scale.data_ptr(), stream), "moe_fp8_quantize_hidden")
+    return out, out_scale

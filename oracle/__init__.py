@@ -15,6 +15,8 @@ Modules:
             fp8 requantisation, GEMM2, weighted combine      (kernel.py:7-250, 663-729)
   layer     the whole layer, in "definition" (fp32 intermediate) or "emulated"
             (fp8-requantised intermediate, as the kernels compute it) mode.
+  quant     the step before the layer: hidden states -> e4m3fn + 1x128 scales [56, T]
+                                                             (kernel.py:131-135, 600-603)
 
 How each function is pinned (tests/test_oracle_*.py):
   fp8.decode/encode, bf16_round  exhaustive/edge comparison with torch's CPU casts
@@ -28,4 +30,7 @@ How each function is pinned (tests/test_oracle_*.py):
                                   torch CPU matmul at small shapes
   layer.layer_forward            pure-Python brute force of the whole composition on
                                   tiny shapes
+  quant.quantize_hidden          torch's CPU float8_e4m3fn cast of x / scale, block-max
+                                  448 and zero-block closed forms, power-of-two scaling
+                                  and sign symmetry, round-trip error bound
 """

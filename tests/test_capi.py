@@ -30,7 +30,9 @@ def test_constants_match_header(pkg):
     assert int(vals["MOE_FP8_HIDDEN"]) == L.HIDDEN and int(vals["MOE_FP8_INTER"]) == L.INTER
     assert int(vals["MOE_FP8_EXPERTS_LOCAL"]) == L.EXPERTS_LOCAL
     for name in ("OK", "EINVAL_POINTER", "EINVAL_TOKENS", "EWORKSPACE", "EINVAL_BIAS_DTYPE",
-                 "EINVAL_OUT_DTYPE", "ELAUNCH", "EDEVICE"):
+                 "EINVAL_OUT_DTYPE", "ELAUNCH", "EDEVICE", "EINVAL_HIDDEN_DTYPE"):
+        assert int(vals["MOE_FP8_" + name]) == getattr(L, name)
+    for name in ("HIDDEN_F32", "HIDDEN_BF16", "HIDDEN_F16", "BIAS_F32", "BIAS_BF16", "BIAS_F16"):
         assert int(vals["MOE_FP8_" + name]) == getattr(L, name)
 
 
@@ -109,7 +111,7 @@ def test_argument_errors_are_reported_before_any_launch(pkg, lib):
     # T = 0 is a no-op that succeeds without a device
     a = _args(pkg, 0)
     assert lib.moe_fp8_run(ctypes.byref(a), None, 0, None) == L.OK
-    for code in (0, -1, -2, -3, -4, -5, -6, -7, -99):
+    for code in (0, -1, -2, -3, -4, -5, -6, -7, -8, -99):
         assert len(L.strerror(code)) > 5
     assert b"gfx950" in lib.moe_fp8_version()
 
@@ -121,3 +123,18 @@ def test_no_device_is_reported(pkg, lib):
     L = pkg._lib
     a = _args(pkg)
     assert lib.moe_fp8_run(ctypes.byref(a), 0x1000, L.workspace_bytes(4), None) == L.EDEVICE
+
+
+def test_quantize_hidden_argument_errors(pkg, lib):
+    L = pkg._lib
+    f = lib.moe_fp8_quantize_hidden
+    assert f(0x1000, L.HIDDEN_BF16, -1, 0x2000, 0x3000, None) == L.EINVAL_TOKENS
+    assert f(0x1000, L.HIDDEN_BF16, (1 << 20) + 1, 0x2000, 0x3000, None) == L.EINVAL_TOKENS
+    assert f(None, L.HIDDEN_BF16, 4, 0x2000, 0x3000, None) == L.EINVAL_POINTER
+    assert f(0x1000, L.HIDDEN_BF16, 4, None, 0x3000, None) == L.EINVAL_POINTER
+    assert f(0x1000, L.HIDDEN_BF16, 4, 0x2000, None, None) == L.EINVAL_POINTER
+    assert f(0x1000, 3, 4, 0x2000, 0x3000, None) == L.EINVAL_HIDDEN_DTYPE
+    assert f(None, 3, 0, None, None, None) == L.OK   # T = 0: nothing to do
+    import torch
+    if not torch.cuda.is_available():
+        assert f(0x1000, L.HIDDEN_BF16, 4, 0x2000, 0x3000, None) == L.EDEVICE
