@@ -44,7 +44,14 @@ def _workload(name):
     gh = _gh()
     dev = torch.device("cuda:0")
     w, wnp = _weights()
-    kw = gh.inputs.make_workload(name, dev, weights=w)
+    if name == "t256":
+        # a decode batch between the named workloads: 32-row items, separate requantisation
+        logits, bias, hq, hs = gh.inputs.make_activations(256, 1005, dev)
+        kw = dict(routing_logits=logits, routing_bias=bias, hidden_states=hq, hidden_states_scale=hs,
+                  gemm1_weights=w[0], gemm1_weights_scale=w[1], gemm2_weights=w[2], gemm2_weights_scale=w[3],
+                  local_expert_offset=0, routed_scaling_factor=gh.inputs.ROUTED_SCALING_FACTOR)
+    else:
+        kw = gh.inputs.make_workload(name, dev, weights=w)
     npkw = gh.to_numpy_inputs({**kw, "gemm1_weights": w[0][:1], "gemm2_weights": w[2][:1]})
     npkw["gemm1_weights"], npkw["gemm1_weights_scale"], npkw["gemm2_weights"], npkw["gemm2_weights_scale"] = wnp
     return kw, npkw
@@ -68,7 +75,7 @@ def _run_full(kw, out_dtype=torch.bfloat16):
     return out
 
 
-@pytest.mark.parametrize("name,sample", [("t16", None), ("t64", None), ("t1024_off64", None),
+@pytest.mark.parametrize("name,sample", [("t16", None), ("t64", None), ("t256", None), ("t1024_off64", None),
                                          ("t8192", 40), ("t4096_skew", 24)])
 def test_layer_matches_oracle(name, sample):
     kw, npkw = _workload(name)
@@ -101,7 +108,7 @@ def test_layer_matches_oracle(name, sample):
     assert np.all(got[zero] == 0)
 
 
-@pytest.mark.parametrize("name", ["t64", "t1024_off64"])
+@pytest.mark.parametrize("name", ["t64", "t256", "t1024_off64"])
 def test_intermediate_fp8_matches_oracle(name):
     gh = _gh()
     kw, npkw = _workload(name)
