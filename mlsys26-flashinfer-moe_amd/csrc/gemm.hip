@@ -260,6 +260,9 @@ __global__ __launch_bounds__(256) void requant_kernel(GemmParams p) {
 // Output rows of every token without exactly one local assignment: the sum of its parked
 // GEMM2 rows in top-k slot order, or zeros. One wavefront per (token, 1/7 of the row): the
 // token's local slots become a uniform bit mask, and each lane sums 4 columns in 4 places.
+// The loads are kept in flight together: the next item's top-k ids and local count are
+// fetched while the current item is summed, and the parked rows are loaded two at a time
+// (the additions stay in slot order).
 constexpr int kCombineChunks = 7;   // 1792 float4 per row = 7 chunks x 4 x 64 lanes
 
 __global__ __launch_bounds__(256) void combine_kernel(GemmParams p) {
@@ -268,30 +271,61 @@ __global__ __launch_bounds__(256) void combine_kernel(GemmParams p) {
   const int lane = threadIdx.x & 63;
   const int nwaves = gridDim.x * 4;
   const int items = p.T * kCombineChunks;
-  for (int it = blockIdx.x * 4 + (threadIdx.x >> 6); it < items; it += nwaves) {
-    const int t = it / kCombineChunks, ch = it - t * kCombineChunks;
-    // the local count and the top-k ids are loaded together (no dependent round trip)
-    const int le = lane < kTopK ? p.topk_ids[t * kTopK + lane] - p.offset : -1;
-    if (__builtin_amdgcn_readfirstlane(p.token_nlocal[t]) == 1) continue;
-    const uint32_t mask = (uint32_t)__ballot(le >= 0 && le < kExpertsLocal);
-    const int v0 = ch * kPerLane * 64 + lane;
-    const v4f* rows = reinterpret_cast<const v4f*>(p.partial + (size_t)t * kTopK * kHidden) + v0;
-    v4f acc[kPerLane];
+  int it = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (it >= items) return;
+  // every lane loads (lane & 7): no divergent branch, so the loads stay in flight until used
+  auto meta = [&](int item, int& id, int& nl) {
+    const int t = item / kCombineChunks;
+    id = p.topk_ids[t * kTopK + (lane & 7)];
+    nl = p.token_nlocal[t];
+  };
+  int id, nl;
+  meta(it, id, nl);
+  while (it < items) {
+    const int next = it + nwaves;
+    int id_n, nl_n;
+    meta(min(next, items - 1), id_n, nl_n);   // past the end: a repeat, never used
+    if (__builtin_amdgcn_readfirstlane(nl) != 1) {
+      const int t = it / kCombineChunks, ch = it - t * kCombineChunks;
+      const int le = id - p.offset;
+      uint32_t m = (uint32_t)__ballot(lane < kTopK && le >= 0 && le < kExpertsLocal);
+      const int v0 = ch * kPerLane * 64 + lane;
+      const v4f* rows = reinterpret_cast<const v4f*>(p.partial + (size_t)t * kTopK * kHidden) + v0;
+      v4f acc[kPerLane];
 #pragma unroll
-    for (int u = 0; u < kPerLane; ++u) acc[u] = v4f{0.f, 0.f, 0.f, 0.f};
-    for (uint32_t m = mask; m; m &= m - 1) {
-      const v4f* r = rows + (size_t)__builtin_ctz(m) * kVecPerRow;
+      for (int u = 0; u < kPerLane; ++u) acc[u] = v4f{0.f, 0.f, 0.f, 0.f};
+      while (m) {
+        const int k0 = __builtin_ctz(m);
+        m &= m - 1;
+        const bool two = m != 0;
+        const int k1 = two ? __builtin_ctz(m) : k0;
+        if (two) m &= m - 1;
+        const v4f* r0 = rows + (size_t)k0 * kVecPerRow;
+        const v4f* r1 = rows + (size_t)k1 * kVecPerRow;
+        v4f a[kPerLane], b[kPerLane];
 #pragma unroll
-      for (int u = 0; u < kPerLane; ++u) acc[u] += r[64 * u];
+        for (int u = 0; u < kPerLane; ++u) {
+          a[u] = r0[64 * u];
+          b[u] = r1[64 * u];
+        }
+#pragma unroll
+        for (int u = 0; u < kPerLane; ++u) {
+          acc[u] += a[u];
+          if (two) acc[u] += b[u];
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kPerLane; ++u) {
+        const size_t h4 = (size_t)t * kVecPerRow + v0 + 64 * u;
+        if (p.out_dtype == MOE_FP8_OUT_BF16)
+          reinterpret_cast<uint2*>(p.out)[h4] = pack_bf16x4(acc[u][0], acc[u][1], acc[u][2], acc[u][3]);
+        else
+          reinterpret_cast<v4f*>(p.out)[h4] = acc[u];
+      }
     }
-#pragma unroll
-    for (int u = 0; u < kPerLane; ++u) {
-      const size_t h4 = (size_t)t * kVecPerRow + v0 + 64 * u;
-      if (p.out_dtype == MOE_FP8_OUT_BF16)
-        reinterpret_cast<uint2*>(p.out)[h4] = pack_bf16x4(acc[u][0], acc[u][1], acc[u][2], acc[u][3]);
-      else
-        reinterpret_cast<v4f*>(p.out)[h4] = acc[u];
-    }
+    it = next;
+    id = id_n;
+    nl = nl_n;
   }
 }
 
