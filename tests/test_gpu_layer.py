@@ -170,3 +170,89 @@ def test_cpu_output_and_inputs_are_moved():
     out = torch.empty((16, 7168), dtype=torch.bfloat16)
     gh.pkg.run(**cpu_kw, output=out)
     assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+
+
+def _given_topk(case, T, rng):
+    ids = np.stack([rng.permutation(256)[:8] for _ in range(T)]).astype(np.int32)
+    if case == "one_expert":                     # every token on local expert 5, nothing else local
+        ids[:, 0] = 5
+        ids[:, 1:] = np.where(ids[:, 1:] < 32, ids[:, 1:] + 32, ids[:, 1:])
+    elif case == "none_local":
+        ids = np.where(ids < 32, ids + 32, ids)
+    elif case == "all_local":
+        ids = np.stack([rng.permutation(32)[:8] for _ in range(T)]).astype(np.int32)
+    elif case == "repeat":                       # a token naming one local expert twice
+        ids[:, 0] = rng.integers(0, 32, size=T)
+        ids[:, 1] = ids[:, 0]
+    w = (rng.random((T, 8)) * 0.5 + 0.1).astype(np.float32)
+    return ids, w
+
+
+@pytest.mark.parametrize("T,case", [(1, "all_local"), (40, "repeat"), (300, "all_local"),
+                                    (600, "one_expert"), (600, "none_local")])
+def test_layer_edge_cases_given_topk(T, case):
+    """The GEMM stages on constructed top-k lists: one token, a repeated expert, every token
+    on one expert (many items of one expert on the tile path), nothing local."""
+    gh = _gh()
+    dev = torch.device("cuda:0")
+    w, wnp = _weights()
+    print(f"layer edge case T={T} {case}", flush=True)
+    rng = np.random.default_rng(T + len(case))
+    ids, tw = _given_topk(case, T, rng)
+    logits, bias, hq, hs = gh.inputs.make_activations(T, 77 + T, dev)
+    kw = dict(routing_logits=logits, routing_bias=bias, hidden_states=hq, hidden_states_scale=hs,
+              gemm1_weights=w[0], gemm1_weights_scale=w[1], gemm2_weights=w[2], gemm2_weights_scale=w[3],
+              local_expert_offset=0, routed_scaling_factor=2.5)
+    out = torch.full((T, 7168), float("nan"), dtype=torch.bfloat16, device=dev)
+    ws = gh.new_workspace(T, dev)
+    gh.write(ws, "topk_ids", ids)
+    gh.write(ws, "topk_weights", tw)
+    args = gh.make_args(**kw, output=out)
+    gh.route_dispatch(args, ws, skip_routing=1)
+    gh.gemm1(args, ws)
+    gh.gemm2_combine(args, ws)
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    assert np.isfinite(got).all()
+    npkw = gh.to_numpy_inputs({**kw, "gemm1_weights": w[0][:1], "gemm2_weights": w[2][:1]})
+    npkw["gemm1_weights"], npkw["gemm1_weights_scale"], npkw["gemm2_weights"], npkw["gemm2_weights_scale"] = wnp
+    tokens = None if T <= 40 else np.sort(rng.choice(T, 24, replace=False))
+    emu = olayer.layer_forward(**npkw, mode="emulated", topk=(ids, tw), tokens=tokens)
+    sel = slice(None) if tokens is None else tokens
+    if case == "none_local":
+        assert np.all(got == 0)
+        return
+    _compare(got[sel], emu["output"], 0.02, 0.02, 0.01, f"T={T} {case} vs emulated oracle")
+
+
+def test_layer_last_expert_group():
+    """local_expert_offset = 224: the device owns the last routing group."""
+    gh = _gh()
+    dev = torch.device("cuda:0")
+    w, wnp = _weights()
+    T = 100
+    logits, bias, hq, hs = gh.inputs.make_activations(T, 91, dev, local_expert_offset=224)
+    kw = dict(routing_logits=logits, routing_bias=bias, hidden_states=hq, hidden_states_scale=hs,
+              gemm1_weights=w[0], gemm1_weights_scale=w[1], gemm2_weights=w[2], gemm2_weights_scale=w[3],
+              local_expert_offset=224, routed_scaling_factor=2.5)
+    print("layer offset 224 T=100", flush=True)
+    got = _run_full(kw).float().cpu().numpy()
+    npkw = gh.to_numpy_inputs({**kw, "gemm1_weights": w[0][:1], "gemm2_weights": w[2][:1]})
+    npkw["gemm1_weights"], npkw["gemm1_weights_scale"], npkw["gemm2_weights"], npkw["gemm2_weights_scale"] = wnp
+    emu = olayer.layer_forward(**npkw, mode="emulated")
+    assert emu["token_nlocal"].sum() > 0
+    _compare(got, emu["output"], 0.02, 0.02, 0.01, "offset 224 vs emulated oracle")
+
+
+def test_zero_tokens():
+    gh = _gh()
+    dev = torch.device("cuda:0")
+    w, _ = _weights()
+    kw = dict(routing_logits=torch.zeros((0, 256), device=dev), routing_bias=torch.zeros(256, device=dev),
+              hidden_states=torch.zeros((0, 7168), device=dev).to(torch.float8_e4m3fn),
+              hidden_states_scale=torch.zeros((56, 0), device=dev),
+              gemm1_weights=w[0], gemm1_weights_scale=w[1], gemm2_weights=w[2], gemm2_weights_scale=w[3],
+              local_expert_offset=0, routed_scaling_factor=2.5)
+    out = torch.empty((0, 7168), dtype=torch.bfloat16, device=dev)
+    assert gh.pkg.run(**kw, output=out) is None
+    torch.cuda.synchronize()
