@@ -16,8 +16,10 @@
 // wave waits until only its loads of step k+1 are in flight (s_waitcnt vmcnt), then a raw
 // s_barrier publishes stage k. Each K-step is one 128x128 scale block:
 // acc += mfma * (s_a * s_w) (kernel.py:123-124, :234). With two wavefronts per SIMD, one
-// wavefront's LDS reads and waits overlap the other's MFMAs. (VALU and MFMA issue largely
-// serialise on gfx950: the four scale FMAs per MFMA bound the loop near 65% of MFMA peak.)
+// wavefront's LDS reads and waits overlap the other's MFMAs. The four scale FMAs of an MFMA
+// result are issued a row group (four MFMAs) after it, while later MFMAs run: VALU work that
+// waits on the MFMA just issued leaves the matrix core idle (a loop that scales each result
+// one MFMA later reaches ~62% of peak, four MFMAs later ~71%, against ~76% with no scaling).
 //
 // LDS tiles: 16-byte chunk c of row m lives at m*128 + ((c ^ ((m >> 1) & 7)) * 16), which
 // spreads the 16 rows read by one ds_read_b128 across distinct bank groups.
@@ -155,7 +157,14 @@ __device__ __forceinline__ void tile_body(const GemmParams& p, const TileCtx& c,
     }
   };
 
-  auto compute = [&](int s, const Head& h, float s0, float s1) {
+  // Software pipeline of the scale promotion: the MFMA results of a row group are scaled
+  // and accumulated while the MFMAs of the next group run (the last group of a K-step while
+  // the first group of the next step runs), so that the matrix core is not idle during the
+  // VALU work. dp holds the pending group's MFMA results, p0/p1 its two scale products.
+  v4f dp[4] = {zero, zero, zero, zero};
+  float p0 = 0.f, p1 = 0.f;
+
+  auto compute = [&](int s, const Head& h, float s0, float s1) __attribute__((always_inline)) {
     if constexpr (NG > 0) {
       const TileStage& st = sh.st[s];
       const v8i (&wf)[4] = h.wf;
@@ -170,13 +179,20 @@ __device__ __forceinline__ void tile_body(const GemmParams& p, const TileCtx& c,
           bf_next = lds_frag(st.a, 64 * wa + 16 * (g + 1) + (lane & 15), lane);
           sa_next = st.sa[(4 * wa + g + 1) * 64 + (lane & 15)];
         }
+        // pending group: the previous group of this step, or the previous step's last
+        // group (zero results and zero scales before the first step)
+        const int gp = g == 0 ? NG - 1 : g - 1;
         v4f d[4];
 #pragma unroll
-        for (int f = 0; f < 4; ++f) d[f] = mfma16x16x128_fp8(wf[f], bf, zero);
-        const float f0 = sa * s0, f1 = sa * s1;
+        for (int f = 0; f < 4; ++f) {
+          d[f] = mfma16x16x128_fp8(wf[f], bf, zero);
+          acc[f][gp] += dp[f] * (f < 2 ? p0 : p1);
+        }
 #pragma unroll
-        for (int f = 0; f < 4; ++f) acc[f][g] += d[f] * (f < 2 ? f0 : f1);
-        // one row group's MFMA results live at a time (the scheduler would otherwise hoist
+        for (int f = 0; f < 4; ++f) dp[f] = d[f];
+        p0 = sa * s0;
+        p1 = sa * s1;
+        // two row groups' MFMA results live at a time (the scheduler would otherwise hoist
         // every MFMA of the step and hold all their results)
         __builtin_amdgcn_sched_barrier(0);
         bf = bf_next;
@@ -207,6 +223,11 @@ __device__ __forceinline__ void tile_body(const GemmParams& p, const TileCtx& c,
     compute(s_cur, h, s0, s1);
     s_cur = s_cur == kStages - 1 ? 0 : s_cur + 1;
     s_next = s_next == kStages - 1 ? 0 : s_next + 1;
+  }
+  // the last step's last row group
+  if constexpr (NG > 0) {
+#pragma unroll
+    for (int f = 0; f < 4; ++f) acc[f][NG - 1] += dp[f] * (f < 2 ? p0 : p1);
   }
   // no ring load of this unit may land after the next unit starts refilling the ring
   wait_vmcnt<0>();
