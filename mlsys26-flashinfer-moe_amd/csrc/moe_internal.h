@@ -4,7 +4,8 @@
 //   caller tensors   : the contract of kernel.py:591-607 (see include/moe_fp8.h)
 //   workspace arrays : moe_fp8_layout offsets; every array is 256-byte aligned.
 // Kernels of one call run in this order on one stream:
-//   (route_kernel<false> -> dispatch_small_kernel) | (route_kernel<true> -> scan_kernel -> place_kernel)
+//   route_dispatch_small_kernel | (route_kernel<false> -> dispatch_small_kernel)
+//   | (route_kernel<true> -> scan_kernel -> place_kernel)
 //   -> GEMM1 -> [requant_kernel] -> GEMM2 -> combine_kernel
 // where, with <= 32 rows per work item, the GEMMs are gemm_stream_kernel<1|2> and GEMM1
 // leaves fp32 SwiGLU rows for requant_kernel; with more rows both are gemm_tile_kernel and

@@ -4,8 +4,10 @@
 // routing (kernel.py:428-542) with branch-free DPP reductions inside 16-lane rows. Dispatch
 // then histograms the local assignments, scans them into CSR offsets, builds the GEMM work
 // list and places every assignment in its bucket:
-//   T <= 256: route_kernel<false> (16 tokens per work-group) -> dispatch_small_kernel, which
-//             does the whole dispatch in one work-group, in LDS;
+//   T <= 16:  route_dispatch_small_kernel, one work-group that routes and then dispatches
+//             in LDS (one launch);
+//   T <= 256 (or given top-k lists): route_kernel<false> (16 tokens per work-group) ->
+//             dispatch_small_kernel, which does the whole dispatch in one work-group, in LDS;
 //   larger T: route_kernel<true> (also per work-group histograms and ranks) -> scan_kernel
 //             -> place_kernel. No kernel synchronises across work-groups.
 //
@@ -321,6 +323,70 @@ __global__ __launch_bounds__(kRouteWaves * 64) void route_kernel(RouteParams p) 
   }
 }
 
+// Dispatch of up to kRouteThreads slots held one per thread (slot tid = token tid/8, top-k
+// position tid%8; le < 0: not a local expert): local counts, stable ranks, CSR offsets, the
+// work list and the placement. The whole work-group calls this.
+__device__ __forceinline__ void dispatch_slots(const RouteParams& p, int le, float w, int nslots,
+                                               int (*s_wcnt)[kExpertsLocal], int* s_cnt, int* s_start) {
+  const int tid = threadIdx.x;
+  // the 8 slots of token tid/8 are 8 consecutive lanes, so one ballot gives every token's
+  // local count
+  const uint64_t m = __ballot(le >= 0);
+  if ((tid & 7) == 0 && tid < nslots) p.token_nlocal[tid >> 3] = __popcll((m >> (lane_id() & 56)) & 0xFFull);
+  const int r = block_rank(le, kRouteThreads / 64, s_wcnt, s_cnt);
+  if (tid < kExpertsLocal) finish_counts(p, tid, s_cnt[tid], s_start);
+  __syncthreads();
+  if (le >= 0) {
+    const int pos = s_start[le] + r;
+    p.sorted_token[pos] = tid >> 3;
+    p.sorted_weight[pos] = w;
+    p.sorted_slot[pos] = tid;
+  }
+}
+
+// Routing and dispatch of up to 64 tokens in one work-group of 16 wavefronts (one launch
+// instead of two dependent ones): wavefront w routes tokens 4w..4w+3, and the top-k lists
+// reach the one-slot-per-thread dispatch through LDS (they are also written to the
+// workspace, which the combine reads). Used up to kFusedRouteTokens tokens: routing is
+// VALU-heavy, and more than one routing wavefront per SIMD on one CU costs more than the
+// saved launch (T=16: 12.1 us against 14.0 us for the two kernels; T=64: 18.8 us against
+// 13.9 us).
+constexpr int kFusedRouteTokens = 16;
+constexpr int kFusedMaxTokens = kRouteThreads / 64 * 4;   // 64: four tokens per wavefront
+static_assert(kFusedRouteTokens <= kFusedMaxTokens, "one routing round");
+
+__global__ __launch_bounds__(kRouteThreads) void route_dispatch_small_kernel(RouteParams p) {
+  __shared__ __attribute__((aligned(16))) float s_bias[kExpertsGlobal];
+  __shared__ int s_id[kFusedMaxTokens * kTopK];
+  __shared__ float s_wt[kFusedMaxTokens * kTopK];
+  __shared__ int s_wcnt[16][kExpertsLocal];
+  __shared__ int s_cnt[kExpertsLocal];
+  __shared__ int s_start[kExpertsLocal + 1];
+  const int tid = threadIdx.x;
+  const int lane = lane_id();
+  const int r = lane & 15;
+  const int tw = (tid >> 6) * 4;   // first token of the wavefront (uniform)
+  float4 lg[4];
+  if (tw < p.T) load_logits(p, tw, lg);
+  stage_bias(p, s_bias);
+  if (tw < p.T) {
+    float w = 0.f;
+    const int id = route_wave(p, s_bias, tw, lg, w);
+    const int t = tw + (lane >> 4);
+    if (t < p.T && r < kTopK) {
+      s_id[t * kTopK + r] = id;
+      s_wt[t * kTopK + r] = w;
+      p.topk_ids[t * kTopK + r] = id;
+      p.topk_w[t * kTopK + r] = w;
+    }
+  }
+  __syncthreads();
+  const int nslots = p.T * kTopK;
+  const int le = tid < nslots ? local_of(s_id[tid], p.offset) : -1;
+  const float w = tid < nslots ? s_wt[tid] : 0.f;
+  dispatch_slots(p, le, w, nslots, s_wcnt, s_cnt, s_start);
+}
+
 // Dispatch of small batches (T <= kSinglePassTokens) in one work-group, from the top-k
 // lists in the workspace: local counts, stable ranks (1024 slots at a time), CSR offsets,
 // the work list and the placement, without leaving the work-group.
@@ -336,21 +402,10 @@ __global__ __launch_bounds__(kRouteThreads) void dispatch_small_kernel(RoutePara
   const int tid = threadIdx.x;
   const int nslots = p.T * kTopK;
   if (nslots <= kRouteThreads) {
-    // One slot per thread, kept in registers: the 8 slots of token tid/8 are 8 consecutive
-    // lanes, so one ballot gives every token's local count.
+    // one slot per thread, kept in registers
     const int le = tid < nslots ? local_of(p.topk_ids[tid], p.offset) : -1;
     const float w = tid < nslots ? p.topk_w[tid] : 0.f;
-    const uint64_t m = __ballot(le >= 0);
-    if ((tid & 7) == 0 && tid < nslots) p.token_nlocal[tid >> 3] = __popcll((m >> (lane_id() & 56)) & 0xFFull);
-    const int r = block_rank(le, kRouteThreads / 64, s_wcnt, s_cnt);
-    if (tid < kExpertsLocal) finish_counts(p, tid, s_cnt[tid], s_start);
-    __syncthreads();
-    if (le >= 0) {
-      const int pos = s_start[le] + r;
-      p.sorted_token[pos] = tid >> 3;
-      p.sorted_weight[pos] = w;
-      p.sorted_slot[pos] = tid;
-    }
+    dispatch_slots(p, le, w, nslots, s_wcnt, s_cnt, s_start);
     return;
   }
   for (int slot = tid; slot < nslots; slot += kRouteThreads) {
@@ -434,7 +489,9 @@ __global__ __launch_bounds__(kRouteTokensPerBlock * kTopK) void place_kernel(Rou
 }
 
 hipError_t launch_route_dispatch(const RouteParams& p, hipStream_t s) {
-  if (p.single_pass) {
+  if (p.single_pass && !p.skip_routing && p.T <= kFusedRouteTokens) {
+    hipLaunchKernelGGL(route_dispatch_small_kernel, dim3(1), dim3(kRouteThreads), 0, s, p);
+  } else if (p.single_pass) {
     if (!p.skip_routing)
       hipLaunchKernelGGL(route_kernel<false>, dim3(p.nblocks), dim3(kRouteWaves * 64), 0, s, p);
     hipLaunchKernelGGL(dispatch_small_kernel, dim3(1), dim3(kRouteThreads), 0, s, p);
