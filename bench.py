@@ -17,11 +17,13 @@ The JSON line also carries:
   roofline      the dominant kernel (GEMM1 at T<=1024, else the larger GEMM) timed with HIP
                 events on the launch stream inside the timed region of a staged run;
   cpu_baseline  the numpy oracle (fp32 dequantise-and-matmul) on the same workload, timed on
-                the host cores;
+                the host cores (median of 5 runs; the host's CPU model and count beside it);
   workloads     the same figures for the other four workloads (T=16, 1024 with offset 64,
                 8192, 4096 skewed), each with the upstream activation quantiser
                 (quantize_hidden: bf16 [T,7168] -> e4m3fn + scales [56,T]) timed beside the
                 layer; its bytes are T * 21,728 (14,336 read, 7,168 + 224 written).
+Per workload, us_per_step is the mean over the K timed calls (one event pair around all K);
+us_median_call is the median of K calls timed one by one in a separate pass.
 """
 from __future__ import annotations
 
@@ -125,6 +127,16 @@ def bench_workload(pkg, inputs, name, weight_sets, steps, warmup):
     wall = time.perf_counter() - t0
     ms_per_step = ev0.elapsed_time(ev1) / steps
 
+    # per-call timing: an event before every call, for the median call duration
+    pev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    for i in range(steps):
+        pev[i].record(stream)
+        step(i)
+    pev[steps].record(stream)
+    torch.cuda.synchronize()
+    call_ms = sorted(pev[i].elapsed_time(pev[i + 1]) for i in range(steps))
+    median_ms = call_ms[steps // 2] if steps % 2 else 0.5 * (call_ms[steps // 2 - 1] + call_ms[steps // 2])
+
     # staged timing with HIP events around each stage on the launch stream
     evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(steps)]
     for i in range(steps):
@@ -165,7 +177,8 @@ def bench_workload(pkg, inputs, name, weight_sets, steps, warmup):
     f = workload_figures(T, n, e_touched, u)
     us = ms_per_step * 1e3
     res = dict(T=T, offset=wl.local_expert_offset, assignments=n, experts_touched=e_touched,
-               us_per_step=round(us, 2), wall_us_per_step=round(wall / steps * 1e6, 2),
+               us_per_step=round(us, 2), us_median_call=round(median_ms * 1e3, 2),
+               wall_us_per_step=round(wall / steps * 1e6, 2),
                hbm_gbs=round(f["layer_bytes"] / (us * 1e-6) / 1e9, 1),
                tflops=round(f["layer_flops"] / (us * 1e-6) / 1e12, 2),
                stage_us=dict(route_dispatch=round(stage_ms[0] * 1e3, 2), gemm1=round(stage_ms[1] * 1e3, 2),
@@ -204,7 +217,14 @@ def cpu_baseline(kw, weight_set, reps=5):
     cnt = r["expert_count"]
     n, e_touched = int(cnt.sum()), int((cnt > 0).sum())
     b = e_touched * BYTES_PER_EXPERT + T * BYTES_PER_TOKEN + 512
+    cpu_model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as fh:
+            cpu_model = next((l.split(":", 1)[1].strip() for l in fh if l.startswith("model name")), cpu_model)
+    except OSError:
+        pass
     return dict(value=round(b / dt / 1e9, 3), unit="GB/s", cores=int(threads), kind="port",
+                cpu_model=cpu_model, host_cpus=os.cpu_count(),
                 sample=f"whole layer, T={T}, {e_touched} touched experts, {n} assignments: median of "
                        f"{reps} runs of oracle.layer_forward(mode='definition'), {dt:.2f} s each, "
                        f"{sum(times):.1f} s in all (numpy: BLAS matmuls on {threads} threads, "
