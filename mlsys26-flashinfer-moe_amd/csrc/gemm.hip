@@ -376,7 +376,7 @@ hipError_t launch_stream(const GemmParams& p, int rows_per_item, hipStream_t s) 
 }  // namespace
 
 hipError_t launch_gemm1(const GemmParams& p, int rows_per_item, hipStream_t s) {
-  if (rows_per_item > 32) return launch_gemm1_tile(p, s);
+  if (rows_per_item > 32) return launch_gemm1_tile(p, rows_per_item, s);
   return launch_stream<kG1>(p, rows_per_item, s);
 }
 
@@ -389,7 +389,7 @@ hipError_t launch_requant(const GemmParams& p, int rows_per_item, hipStream_t s)
 }
 
 hipError_t launch_gemm2(const GemmParams& p, int rows_per_item, hipStream_t s) {
-  if (rows_per_item > 32) return launch_gemm2_tile(p, s);
+  if (rows_per_item > 32) return launch_gemm2_tile(p, rows_per_item, s);
   return launch_stream<kG2>(p, rows_per_item, s);
 }
 

@@ -1,20 +1,28 @@
 // Large-batch grouped fp8 block-scale GEMMs of the MoE layer (gfx950 MFMA).
 //
-// Tile = (work item of <= 128 assignment rows of one local expert) x (256 weight rows).
+// Tile = (work item of one local expert) x (256 weight rows). Two instances: items of up to
+// 128 rows (T < 4096) and of up to 160 rows (T >= 4096; the largest whose three ring stages
+// fit the CU's LDS). The bigger the item, the fewer bytes the CU moves per flop, which is
+// what bounds this loop at large T; at mid-size T the fewer, longer units of the large
+// instance would balance worse over the CUs.
 // A work-group of 8 wavefronts (two per SIMD) computes one tile; wavefront w = 4a + b owns
-// weight rows [64b, 64b+64) of the tile (four 16-row MFMA fragments) against item rows
-// [64a, 64a+64) (up to four 16-row groups): 4 x NG v_mfma_f32_16x16x128_f8f6f4 per 128-wide
-// K-step with 16*NG fp32 accumulators per lane.
+// weight rows [64b, 64b+64) of the tile (four 16-row MFMA fragments) against half a of the
+// item's 16-row groups (up to five; the halves differ by at most one group):
+// 4 x NG v_mfma_f32_16x16x128_f8f6f4 per 128-wide K-step with 16*NG fp32 accumulators per
+// lane.
 //   GEMM1: the tile is 128 SwiGLU columns: tile rows 0..127 are their gate rows of W13,
 //          rows 128..255 the matching up rows; wavefront (a, b) owns columns [32b, 32b+32)
 //          (fragments 0,1 gate, 2,3 up).
 //   GEMM2: the tile is 256 hidden rows of W2.
-// Both operands of a K-step (256 x 128 weight bytes, 128 x 128 activation bytes and the
-// activations' scales) flow through a 3-stage LDS ring filled with global_load_lds two
-// K-steps ahead: every 16-byte DMA instruction reads 8 whole 128-byte rows, so the vector
-// memory pipeline sees full cache lines. The waits are explicit: at the top of step k every
-// wave waits until only its loads of step k+1 are in flight (s_waitcnt vmcnt), then a raw
-// s_barrier publishes stage k. Each K-step is one 128x128 scale block:
+// Both operands of a K-step (256 x 128 weight bytes, 128 or 160 x 128 activation bytes and
+// the activations' scales) flow through a 3-stage LDS ring (146 or 158 KB) filled with
+// global_load_lds two K-steps ahead: every 16-byte DMA instruction reads 8 whole 128-byte
+// rows, so the vector memory pipeline sees full cache lines. The waits are explicit: at the
+// top of step k every wave waits until only its loads of step k+1 are in flight (s_waitcnt
+// vmcnt), then a raw s_barrier publishes stage k. Every wave issues the same number of loads
+// each step and the loop has no data-dependent branch (the last two steps reload the last
+// step into stages nobody reads): a loop split into blocks by per-wave load counts measured
+// 15% slower at T=1024. Each K-step is one 128x128 scale block:
 // acc += mfma * (s_a * s_w) (kernel.py:123-124, :234). With two wavefronts per SIMD, one
 // wavefront's LDS reads and waits overlap the other's MFMAs. The four scale FMAs of an MFMA
 // result are issued a row group (four MFMAs) after it, while later MFMAs run: VALU work that
@@ -34,13 +42,30 @@ namespace moe {
 
 namespace {
 
-constexpr int kTileRows = 128;                       // item rows per tile (max rows of an item)
 constexpr int kTileW = 256;                          // weight rows per tile
 constexpr int kTileWaves = 8;                        // wavefronts per work-group
 constexpr int kStages = 3;                           // LDS ring stages
 constexpr int kWDma = kTileW / kTileWaves / 8;       // weight DMA loads per wavefront per step (4)
-constexpr int kADma = kTileRows / kTileWaves / 8;    // activation DMA loads per wavefront per step (2)
-constexpr int kLoadsPerStep = kWDma + kADma + 1;     // + 1 scale DMA
+
+// Shape of the kernel for items of up to ROWS rows (kTileItemRowsMid or kTileItemRowsLarge).
+// Per K-step every wavefront issues kLoadsPerStep loads: its 32 weight rows (kWDma loads),
+// the activation row blocks w and w+8 of the tile (8 rows each) and a third load:
+//   128 rows: the scales of one 64-row block (block w%4 capped at the last one; a load that
+//             repeats another writes the same bytes to the same LDS slots);
+//   160 rows: activation block w+16 for waves 0-3, and the scales of 64-row block w-4
+//             (capped at the last one) for waves 4-7.
+template <int ROWS>
+struct TileShape {
+  static constexpr int kRows = ROWS;
+  static constexpr int kABlocks = ROWS / 8;
+  static constexpr bool kThirdBlock = kABlocks > 2 * kTileWaves;   // waves 0-3 load block w+16
+  static constexpr int kSBlocks = (ROWS + 63) / 64;       // 64-row scale blocks
+  static constexpr int kSSlots = 64 * kSBlocks;
+  static constexpr int kMaxNG = (ROWS / 16 + 1) / 2;      // row groups of a wavefront half
+  static constexpr int kLoadsPerStep = kWDma + 3;
+  static_assert(ROWS % 16 == 0 && (kABlocks == 2 * kTileWaves || kABlocks == 2 * kTileWaves + 4), "tile rows");
+  static_assert(kSBlocks <= 4, "scale blocks");
+};
 
 typedef __attribute__((address_space(3))) void lds_void;
 
@@ -60,38 +85,36 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt(N | (7 << 4) | (15 << 8));
 }
 
-// Work-group barrier that publishes LDS ring stages filled by global_load_lds: the caller's
-// vmcnt wait covers this wave's loads, s_barrier covers the other waves', and the two
-// compiler-only fences keep every memory access on its side of the barrier.
-template <int N>
-__device__ __forceinline__ void ring_barrier() {
-  wait_vmcnt<N>();
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __builtin_amdgcn_s_barrier();
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
-
+template <int ROWS>
 struct TileStage {
   uint8_t w[kTileW * 128];
-  uint8_t a[kTileRows * 128];
-  float sa[kTileWaves * 64];   // scale of item row m at (m / 16) * 64 + m % 16
+  uint8_t a[ROWS * 128];
+  float sa[TileShape<ROWS>::kSSlots];   // scale of item row m at m
 };
 
+template <int ROWS>
 struct TileShared {
-  TileStage st[kStages];
-  float amax[4][kTileRows];
+  TileStage<ROWS> st[kStages];
 };
+static_assert(sizeof(TileShared<kTileItemRowsLarge>) <= 160 * 1024, "LDS of one CU");
+// GEMM1's per-row amax exchange after the K loop uses the weight tile of a stage that the
+// last K-step does not read and that no load targets after the top of the last K-step.
+constexpr int kAmaxStage = kHBlocks % kStages;
+static_assert(kAmaxStage != (kHBlocks - 1) % kStages, "the last K-step reads another stage");
+static_assert(4 * kTileItemRowsLarge * sizeof(float) <= kTileW * 128, "amax fits in a weight tile");
 
 // Per-work-unit pointers of one lane.
+template <int ROWS>
 struct TileCtx {
   const uint8_t* wbase;        // weight tensor (the per-step source is wbase + k*128 + woff)
   uint32_t woff[kWDma];        // weight DMA byte offsets (row + permuted 16-byte chunk); < 2^30
-  const uint8_t* asrc[kADma];  // activation DMA sources
-  const float* ssrc;           // activation scale DMA source
+  const uint8_t* asrc[3];      // activation DMA sources of blocks w, w+8 (and w+16)
+  int sblk;                    // the 64-row scale block this wave loads
+  const float* ssrc;           // activation scale DMA source (waves 4-7)
   size_t sstride;              // scale stride between K blocks
   const float* swp0;           // block scales of fragments 0,1 (GEMM1 gate) ...
   const float* swp1;           // ... and 2,3 (GEMM1 up)
-  int r0, rows, tile;
+  int r0, rows, tile, m0;      // item rows [r0, r0+rows); first item row of this wave's half
 };
 
 // A 16-row MFMA operand fragment (rows m0 .. m0+15 of an LDS tile): lane l holds row
@@ -101,12 +124,13 @@ __device__ __forceinline__ v8i lds_frag(const uint8_t* buf, int m, int lane) {
               *reinterpret_cast<const v4i*>(buf + swz(m, 4 + (lane >> 4))));
 }
 
-template <bool G1, int NG>
-__device__ __forceinline__ void tile_body(const GemmParams& p, const TileCtx& c, TileShared& sh) {
+template <bool G1, int NG, int ROWS>
+__device__ __forceinline__ void tile_body(const GemmParams& p, const TileCtx<ROWS>& c, TileShared<ROWS>& sh) {
+  using S = TileShape<ROWS>;
   constexpr int KS = G1 ? kHBlocks : kIBlocks;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int wb = wave & 3, wa = wave >> 2;   // weight rows 64*wb.., item rows 64*wa..
+  const int wb = wave & 3;     // weight rows 64*wb.. (item rows: the wave's half, from c.m0)
 
   // lane k holds the weight block scales of K-step k (read back with readlane: the loop
   // itself touches no memory for them)
@@ -114,15 +138,21 @@ __device__ __forceinline__ void tile_body(const GemmParams& p, const TileCtx& c,
   const float sw1_lane = c.swp1[lane < KS ? lane : 0];
 
   // Loads of step k into stage s: this wave's share of the weight rows, activation rows and
-  // activation scales. Every lane loads (lanes past the wave's 16 scale rows repeat them
-  // into unused slots), so no load is divergent; every wave loads even if it has no rows.
-  auto issue = [&](int k, int s) {
-    TileStage& st = sh.st[s];
+  // activation scales, S::kLoadsPerStep in all. Every lane loads (activation rows and scale
+  // rows past the item's end repeat its first row into slots nobody reads), so no load is
+  // divergent; every wave loads even if it has no rows.
+  auto issue = [&](int k, int s) __attribute__((always_inline)) {
+    TileStage<ROWS>& st = sh.st[s];
 #pragma unroll
     for (int j = 0; j < kWDma; ++j) dma16(c.wbase + k * 128 + c.woff[j], &st.w[(32 * wave + 8 * j) * 128]);
 #pragma unroll
-    for (int j = 0; j < kADma; ++j) dma16(c.asrc[j] + k * 128, &st.a[(16 * wave + 8 * j) * 128]);
-    dma4(c.ssrc + k * c.sstride, &st.sa[64 * wave]);
+    for (int j = 0; j < 2; ++j) dma16(c.asrc[j] + k * 128, &st.a[8 * (wave + kTileWaves * j) * 128]);
+    if constexpr (S::kThirdBlock) {
+      if (wave < 4) dma16(c.asrc[2] + k * 128, &st.a[8 * (wave + 2 * kTileWaves) * 128]);
+      else dma4(c.ssrc + k * c.sstride, &st.sa[64 * c.sblk]);
+    } else {
+      dma4(c.ssrc + k * c.sstride, &st.sa[64 * c.sblk]);
+    }
   };
 
   v4f acc[4][NG > 0 ? NG : 1];
@@ -149,9 +179,9 @@ __device__ __forceinline__ void tile_body(const GemmParams& p, const TileCtx& c,
   };
   auto load_head = [&](int s, Head& h) {
     if constexpr (NG > 0) {
-      const TileStage& st = sh.st[s];
-      h.bf = lds_frag(st.a, 64 * wa + (lane & 15), lane);
-      h.sa = st.sa[(4 * wa) * 64 + (lane & 15)];
+      const TileStage<ROWS>& st = sh.st[s];
+      h.bf = lds_frag(st.a + c.m0 * 128, lane & 15, lane);
+      h.sa = st.sa[c.m0 + (lane & 15)];
 #pragma unroll
       for (int f = 0; f < 4; ++f) h.wf[f] = lds_frag(st.w, wrow(f), lane);
     }
@@ -166,7 +196,7 @@ __device__ __forceinline__ void tile_body(const GemmParams& p, const TileCtx& c,
 
   auto compute = [&](int s, const Head& h, float s0, float s1) __attribute__((always_inline)) {
     if constexpr (NG > 0) {
-      const TileStage& st = sh.st[s];
+      const TileStage<ROWS>& st = sh.st[s];
       const v8i (&wf)[4] = h.wf;
       v8i bf = h.bf;
       float sa = h.sa;
@@ -176,8 +206,8 @@ __device__ __forceinline__ void tile_body(const GemmParams& p, const TileCtx& c,
         v8i bf_next = bf;
         float sa_next = sa;
         if (g + 1 < NG) {
-          bf_next = lds_frag(st.a, 64 * wa + 16 * (g + 1) + (lane & 15), lane);
-          sa_next = st.sa[(4 * wa + g + 1) * 64 + (lane & 15)];
+          bf_next = lds_frag(st.a + c.m0 * 128, 16 * (g + 1) + (lane & 15), lane);
+          sa_next = st.sa[c.m0 + 16 * (g + 1) + (lane & 15)];
         }
         // pending group: the previous group of this step, or the previous step's last
         // group (zero results and zero scales before the first step)
@@ -212,7 +242,10 @@ __device__ __forceinline__ void tile_body(const GemmParams& p, const TileCtx& c,
   for (int k = 0; k < KS; ++k) {
     // step k's loads are complete for this wave (only step k+1's may be in flight), and
     // after the barrier for every wave; every wave is also done with stage s_next (step k-1)
-    ring_barrier<kLoadsPerStep>();
+    wait_vmcnt<S::kLoadsPerStep>();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
     Head h;
     load_head(s_cur, h);
     __builtin_amdgcn_sched_barrier(0);
@@ -235,7 +268,14 @@ __device__ __forceinline__ void tile_body(const GemmParams& p, const TileCtx& c,
   if constexpr (G1) {
     // SwiGLU (kernel.py:126-129) and 1x128 requantisation (kernel.py:131-135 with 128
     // columns): the tile's 128 columns are one scale block, spread over the 4 wavefronts
-    // that share this wave's item rows.
+    // that share this wave's item rows. Their row amax meet in the weight tile of stage
+    // kAmaxStage, which no wave reads or loads any more.
+    float(*amax_buf)[ROWS] = reinterpret_cast<float(*)[ROWS]>(sh.st[kAmaxStage].w);
+    // every wave's loads (the last two steps reload the last step into two stages, one of
+    // them kAmaxStage) have landed
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
     float cval[NG > 0 ? NG : 1][2][4];
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
@@ -250,13 +290,13 @@ __device__ __forceinline__ void tile_body(const GemmParams& p, const TileCtx& c,
         }
       amax = fmaxf(amax, __shfl_xor(amax, 16));
       amax = fmaxf(amax, __shfl_xor(amax, 32));
-      if (lane < 16) sh.amax[wb][64 * wa + 16 * g + lane] = amax;
+      if (lane < 16) amax_buf[wb][c.m0 + 16 * g + lane] = amax;
     }
     __syncthreads();
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
-      const int m = 64 * wa + 16 * g + (lane & 15);
-      const float amax = fmaxf(fmaxf(sh.amax[0][m], sh.amax[1][m]), fmaxf(sh.amax[2][m], sh.amax[3][m]));
+      const int m = c.m0 + 16 * g + (lane & 15);
+      const float amax = fmaxf(fmaxf(amax_buf[0][m], amax_buf[1][m]), fmaxf(amax_buf[2][m], amax_buf[3][m]));
       const float scale = fmaxf(amax / 448.0f, 1e-12f);
       if (m < c.rows) {
         uint8_t* dst = p.act + (size_t)(c.r0 + m) * kInter + c.tile * 128 + 32 * wb + 4 * (lane >> 4);
@@ -271,7 +311,7 @@ __device__ __forceinline__ void tile_body(const GemmParams& p, const TileCtx& c,
   } else {
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
-      const int m = 64 * wa + 16 * g + (lane & 15);
+      const int m = c.m0 + 16 * g + (lane & 15);
       if (m < c.rows) {
         const int pr = c.r0 + m;
         const int t = p.sorted_token[pr];
@@ -297,10 +337,22 @@ __device__ __forceinline__ void tile_body(const GemmParams& p, const TileCtx& c,
   }
 }
 
-template <bool G1>
+// NG (row groups of this wave's half) as a template argument: instantiations 0..kMaxNG.
+template <bool G1, int ROWS, int NG = 0>
+__device__ __forceinline__ void tile_body_ng(const GemmParams& p, const TileCtx<ROWS>& c, TileShared<ROWS>& sh, int ng) {
+  if constexpr (NG < TileShape<ROWS>::kMaxNG) {
+    if (ng == NG) tile_body<G1, NG, ROWS>(p, c, sh);
+    else tile_body_ng<G1, ROWS, NG + 1>(p, c, sh, ng);
+  } else {
+    tile_body<G1, NG, ROWS>(p, c, sh);
+  }
+}
+
+template <bool G1, int ROWS>
 __global__ __launch_bounds__(kTileWaves * 64, 1) void gemm_tile_kernel(GemmParams p) {
+  using S = TileShape<ROWS>;
   constexpr int TILES = (G1 ? 2 * kInter : kHidden) / kTileW;
-  __shared__ __attribute__((aligned(1024))) TileShared sh;
+  __shared__ __attribute__((aligned(1024))) TileShared<ROWS> sh;
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -319,7 +371,7 @@ __global__ __launch_bounds__(kTileWaves * 64, 1) void gemm_tile_kernel(GemmParam
     // work-item fields are wave-uniform; say so, so that everything derived from them
     // (notably the weight block-scale addresses) stays in scalar registers
     const int e = __builtin_amdgcn_readfirstlane(it.x);
-    TileCtx c;
+    TileCtx<ROWS> c;
     c.r0 = __builtin_amdgcn_readfirstlane(it.y);
     c.rows = __builtin_amdgcn_readfirstlane(it.z);
     c.tile = __builtin_amdgcn_readfirstlane(v / ne);
@@ -336,9 +388,12 @@ __global__ __launch_bounds__(kTileWaves * 64, 1) void gemm_tile_kernel(GemmParam
       else grow = (size_t)e * kHidden + c.tile * kTileW + r;
       c.woff[j] = (uint32_t)(grow * (G1 ? kHidden : kInter) + ch * 16);
     }
+    // activation DMA j of this wave fills tile rows 8i .. 8i+7 with i = wave + 8j (j = 2 for
+    // waves 0-3 of the 160-row tile only; otherwise unused)
 #pragma unroll
-    for (int j = 0; j < kADma; ++j) {
-      const int m = 16 * wave + 8 * j + (lane >> 3);
+    for (int j = 0; j < 3; ++j) {
+      const int blk = min(wave + kTileWaves * j, S::kABlocks - 1);
+      const int m = 8 * blk + (lane >> 3);
       const int mm = m < c.rows ? m : 0;
       const int ch = (lane & 7) ^ ((m >> 1) & 7);
       size_t row;
@@ -347,7 +402,10 @@ __global__ __launch_bounds__(kTileWaves * 64, 1) void gemm_tile_kernel(GemmParam
       c.asrc[j] = (G1 ? p.hidden : p.act) + row + ch * 16;
     }
     {
-      const int m = 16 * wave + (lane & 15);
+      // the wave's 64-row block of scales: w % 4 (128 rows) or w - 4 (160 rows, waves 4-7),
+      // capped at the last block
+      c.sblk = min(S::kThirdBlock ? max(wave - 4, 0) : (wave & 3), S::kSBlocks - 1);
+      const int m = 64 * c.sblk + lane;
       const int mm = m < c.rows ? m : 0;
       if constexpr (G1) c.ssrc = p.hidden_scale + p.sorted_token[c.r0 + mm];
       else c.ssrc = p.act_scale + (size_t)(c.r0 + mm) * kIBlocks;
@@ -360,16 +418,12 @@ __global__ __launch_bounds__(kTileWaves * 64, 1) void gemm_tile_kernel(GemmParam
       c.swp0 = p.w2_scale + ((size_t)e * kHBlocks + (c.tile * kTileW + 64 * (wave & 3)) / 128) * kIBlocks;
       c.swp1 = c.swp0;
     }
-    // row groups of this wave's 64 item rows
-    const int mine = c.rows - 64 * (wave >> 2);
-    const int ng = mine <= 0 ? 0 : min(4, (mine + 15) >> 4);
-    switch (ng) {
-      case 0: tile_body<G1, 0>(p, c, sh); break;
-      case 1: tile_body<G1, 1>(p, c, sh); break;
-      case 2: tile_body<G1, 2>(p, c, sh); break;
-      case 3: tile_body<G1, 3>(p, c, sh); break;
-      default: tile_body<G1, 4>(p, c, sh); break;
-    }
+    // the item's row groups, split between the two wavefront halves (half 0 takes the odd one)
+    const int groups = (c.rows + 15) >> 4;
+    const int g0 = (groups + 1) >> 1;
+    const int ng = (wave >> 2) == 0 ? g0 : groups - g0;
+    c.m0 = (wave >> 2) == 0 ? 0 : 16 * g0;
+    tile_body_ng<G1, ROWS>(p, c, sh, ng);
   }
 }
 
@@ -385,7 +439,7 @@ int num_cus_tile() {
   return cached[dev];
 }
 
-template <bool G1>
+template <bool G1, int ROWS>
 hipError_t launch_tile(const GemmParams& p, hipStream_t s) {
   const int tiles = (G1 ? 2 * kInter : kHidden) / kTileW;
   const int max_units = p.max_items * tiles;
@@ -393,13 +447,19 @@ hipError_t launch_tile(const GemmParams& p, hipStream_t s) {
   const int cap = ((max_units + 7) / 8) * 8;
   if (grid > cap) grid = cap;
   if (grid <= 0) return hipSuccess;
-  hipLaunchKernelGGL((gemm_tile_kernel<G1>), dim3(grid), dim3(kTileWaves * 64), 0, s, p);
+  hipLaunchKernelGGL((gemm_tile_kernel<G1, ROWS>), dim3(grid), dim3(kTileWaves * 64), 0, s, p);
   return hipGetLastError();
 }
 
 }  // namespace
 
-hipError_t launch_gemm1_tile(const GemmParams& p, hipStream_t s) { return launch_tile<true>(p, s); }
-hipError_t launch_gemm2_tile(const GemmParams& p, hipStream_t s) { return launch_tile<false>(p, s); }
+hipError_t launch_gemm1_tile(const GemmParams& p, int rows_per_item, hipStream_t s) {
+  return rows_per_item > kTileItemRowsMid ? launch_tile<true, kTileItemRowsLarge>(p, s)
+                                          : launch_tile<true, kTileItemRowsMid>(p, s);
+}
+hipError_t launch_gemm2_tile(const GemmParams& p, int rows_per_item, hipStream_t s) {
+  return rows_per_item > kTileItemRowsMid ? launch_tile<false, kTileItemRowsLarge>(p, s)
+                                          : launch_tile<false, kTileItemRowsMid>(p, s);
+}
 
 }  // namespace moe

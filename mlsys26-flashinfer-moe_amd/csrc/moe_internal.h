@@ -43,11 +43,20 @@ constexpr int kCtrItems = 0;    // number of GEMM work items
 constexpr int kCtrAssign = 1;   // N, the number of local assignments
 constexpr int kNumCounters = 16;
 
-// Rows (assignments) per GEMM work item for a call with T tokens.
+// Rows of a work item of the tile GEMMs: gemm_tile_kernel has an instance for items of up to
+// 128 rows and one for items of up to 160 (10 row groups of 16, the largest whose ring fits LDS).
+constexpr int kTileItemRowsMid = 128;
+constexpr int kTileItemRowsLarge = 160;
+
+// Rows (assignments) per GEMM work item for a call with T tokens. Tile-path items hold up to
+// 128 rows below 4096 tokens and up to 160 from there: larger items move fewer bytes per
+// flop, but at mid-size batches the fewer, longer units balance worse over the CUs (measured:
+// T=1024 GEMM1 170 us with 128-row items against 196 us with 160; T=8192 342 against 319).
 inline int rows_per_item_for(int T) {
   if (T <= 64) return 16;
   if (T <= 512) return 32;
-  return 128;
+  if (T < 4096) return kTileItemRowsMid;
+  return kTileItemRowsLarge;
 }
 
 int compute_layout(int32_t T, moe_fp8_layout* out);
@@ -109,8 +118,8 @@ hipError_t launch_gemm1(const GemmParams& p, int rows_per_item, hipStream_t s);
 hipError_t launch_requant(const GemmParams& p, int rows_per_item, hipStream_t s);
 hipError_t launch_gemm2(const GemmParams& p, int rows_per_item, hipStream_t s);
 hipError_t launch_combine(const GemmParams& p, hipStream_t s);
-hipError_t launch_gemm1_tile(const GemmParams& p, hipStream_t s);
+hipError_t launch_gemm1_tile(const GemmParams& p, int rows_per_item, hipStream_t s);
 hipError_t launch_quantize_hidden(const void* x, int dtype, int T, uint8_t* q, float* scale, hipStream_t s);
-hipError_t launch_gemm2_tile(const GemmParams& p, hipStream_t s);
+hipError_t launch_gemm2_tile(const GemmParams& p, int rows_per_item, hipStream_t s);
 
 }  // namespace moe
