@@ -293,7 +293,7 @@ def main():
     if rpi <= 32:
         kernel, tag = f"gemm_stream_kernel<1, {1 if rpi <= 16 else 2}>", "gemm1_stream"
     else:
-        kernel, tag = "gemm_tile_kernel<true>", "gemm1_tile"
+        kernel, tag = f"gemm_tile_kernel<true, {160 if rpi > 128 else 128}>", "gemm1_tile"
     if T <= 1024:
         roof = dict(kernel=kernel, bound="hbm", achieved=round(main_f["g1_bytes"] / (g1_ms * 1e-3) / 1e9, 1),
                     peak=HBM_PEAK_GBS, unit="GB/s")
