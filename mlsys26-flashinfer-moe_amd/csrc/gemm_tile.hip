@@ -97,10 +97,6 @@ struct TileShared {
   TileStage<ROWS> st[kStages];
 };
 static_assert(sizeof(TileShared<kTileItemRowsLarge>) <= 160 * 1024, "LDS of one CU");
-// GEMM1's per-row amax exchange after the K loop uses the weight tile of a stage that the
-// last K-step does not read and that no load targets after the top of the last K-step.
-constexpr int kAmaxStage = kHBlocks % kStages;
-static_assert(kAmaxStage != (kHBlocks - 1) % kStages, "the last K-step reads another stage");
 static_assert(4 * kTileItemRowsLarge * sizeof(float) <= kTileW * 128, "amax fits in a weight tile");
 
 // Per-work-unit pointers of one lane.
@@ -112,9 +108,10 @@ struct TileCtx {
   int sblk;                    // the 64-row scale block this wave loads
   const float* ssrc;           // activation scale DMA source (waves 4-7)
   size_t sstride;              // scale stride between K blocks
-  const float* swp0;           // block scales of fragments 0,1 (GEMM1 gate) ...
-  const float* swp1;           // ... and 2,3 (GEMM1 up)
+  float sw0_lane, sw1_lane;     // lane k: weight block scale of K-step k of fragments 0,1
+                               // (GEMM1 gate) and 2,3 (GEMM1 up)
   int r0, rows, tile, m0;      // item rows [r0, r0+rows); first item row of this wave's half
+  int ng;                      // row groups of this wave's half
 };
 
 // A 16-row MFMA operand fragment (rows m0 .. m0+15 of an LDS tile): lane l holds row
@@ -124,8 +121,14 @@ __device__ __forceinline__ v8i lds_frag(const uint8_t* buf, int m, int lane) {
               *reinterpret_cast<const v4i*>(buf + swz(m, 4 + (lane >> 4))));
 }
 
+// One unit (c). Its K-steps read ring stages s_base, s_base+1, .. (mod 3). GEMM2 (16 K-steps
+// per unit) prefetches across units: its last two steps load the first two steps of the next
+// unit (n) when `have_n`, and `pre` says that this unit's were loaded so. GEMM1 (56 K-steps)
+// does not (the per-step address selects cost it more than the saved ring fill): its last two
+// steps, like GEMM2's last unit's, load the last step again into stages nobody reads.
 template <bool G1, int NG, int ROWS>
-__device__ __forceinline__ void tile_body(const GemmParams& p, const TileCtx<ROWS>& c, TileShared<ROWS>& sh) {
+__device__ __forceinline__ void tile_body(const GemmParams& p, const TileCtx<ROWS>& c, const TileCtx<ROWS>& n,
+                                          bool have_n, int s_base, bool pre, TileShared<ROWS>& sh) {
   using S = TileShape<ROWS>;
   constexpr int KS = G1 ? kHBlocks : kIBlocks;
   const int lane = threadIdx.x & 63;
@@ -134,24 +137,30 @@ __device__ __forceinline__ void tile_body(const GemmParams& p, const TileCtx<ROW
 
   // lane k holds the weight block scales of K-step k (read back with readlane: the loop
   // itself touches no memory for them)
-  const float sw0_lane = c.swp0[lane < KS ? lane : 0];
-  const float sw1_lane = c.swp1[lane < KS ? lane : 0];
+  const float sw0_lane = c.sw0_lane;
+  const float sw1_lane = c.sw1_lane;
 
-  // Loads of step k into stage s: this wave's share of the weight rows, activation rows and
-  // activation scales, S::kLoadsPerStep in all. Every lane loads (activation rows and scale
-  // rows past the item's end repeat its first row into slots nobody reads), so no load is
-  // divergent; every wave loads even if it has no rows.
-  auto issue = [&](int k, int s) __attribute__((always_inline)) {
+  // Loads of unit step kk into stage s: this wave's share of the weight rows, activation
+  // rows and activation scales, S::kLoadsPerStep in all. Steps past the unit's last are the
+  // next unit's first ones (or, without a next unit, the last step again); the choice is a
+  // select of the source addresses, so the loop has no branch. Every lane loads (activation
+  // rows and scale rows past the item's end repeat its first row into slots nobody reads), so
+  // no load is divergent; every wave loads even if it has no rows.
+  auto issue = [&](int kk, int s) __attribute__((always_inline)) {
+    const bool nxt = !G1 && kk >= KS && have_n;
+    const int k = kk < KS ? kk : (nxt ? kk - KS : KS - 1);
     TileStage<ROWS>& st = sh.st[s];
+    const uint8_t* wk = (nxt ? n.wbase : c.wbase) + k * 128;
 #pragma unroll
-    for (int j = 0; j < kWDma; ++j) dma16(c.wbase + k * 128 + c.woff[j], &st.w[(32 * wave + 8 * j) * 128]);
+    for (int j = 0; j < kWDma; ++j) dma16(wk + (nxt ? n.woff[j] : c.woff[j]), &st.w[(32 * wave + 8 * j) * 128]);
 #pragma unroll
-    for (int j = 0; j < 2; ++j) dma16(c.asrc[j] + k * 128, &st.a[8 * (wave + kTileWaves * j) * 128]);
+    for (int j = 0; j < 2; ++j) dma16((nxt ? n.asrc[j] : c.asrc[j]) + k * 128, &st.a[8 * (wave + kTileWaves * j) * 128]);
+    const float* sk = (nxt ? n.ssrc : c.ssrc) + k * c.sstride;
     if constexpr (S::kThirdBlock) {
-      if (wave < 4) dma16(c.asrc[2] + k * 128, &st.a[8 * (wave + 2 * kTileWaves) * 128]);
-      else dma4(c.ssrc + k * c.sstride, &st.sa[64 * c.sblk]);
+      if (wave < 4) dma16((nxt ? n.asrc[2] : c.asrc[2]) + k * 128, &st.a[8 * (wave + 2 * kTileWaves) * 128]);
+      else dma4(sk, &st.sa[64 * c.sblk]);
     } else {
-      dma4(c.ssrc + k * c.sstride, &st.sa[64 * c.sblk]);
+      dma4(sk, &st.sa[64 * c.sblk]);
     }
   };
 
@@ -231,13 +240,16 @@ __device__ __forceinline__ void tile_body(const GemmParams& p, const TileCtx<ROW
     }
   };
 
-  // the previous unit's readers of the LDS ring are done before it is refilled
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __builtin_amdgcn_s_barrier();
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  issue(0, 0);
-  issue(1, 1);
-  int s_cur = 0, s_next = 2;
+  // A unit whose first two steps were not prefetched loads them itself, once every wave is
+  // done with the ring (the previous unit's last loads have landed: see the end of the unit).
+  int s_cur = s_base, s_next = s_base == 0 ? kStages - 1 : s_base - 1;
+  if (!pre) {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    issue(0, s_cur);
+    issue(1, s_cur == kStages - 1 ? 0 : s_cur + 1);
+  }
 #pragma nounroll
   for (int k = 0; k < KS; ++k) {
     // step k's loads are complete for this wave (only step k+1's may be in flight), and
@@ -249,7 +261,7 @@ __device__ __forceinline__ void tile_body(const GemmParams& p, const TileCtx<ROW
     Head h;
     load_head(s_cur, h);
     __builtin_amdgcn_sched_barrier(0);
-    issue(min(k + 2, KS - 1), s_next);   // past the last step: the last step again, never read
+    issue(k + 2, s_next);
     __builtin_amdgcn_sched_barrier(0);
     const float s0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sw0_lane), k));
     const float s1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sw1_lane), k));
@@ -262,17 +274,17 @@ __device__ __forceinline__ void tile_body(const GemmParams& p, const TileCtx<ROW
 #pragma unroll
     for (int f = 0; f < 4; ++f) acc[f][NG - 1] += dp[f] * (f < 2 ? p0 : p1);
   }
-  // no ring load of this unit may land after the next unit starts refilling the ring
-  wait_vmcnt<0>();
+  // The loads in flight now are the next unit's first two steps, or reloads nobody reads; the
+  // reloads must land before the next unit refills the ring.
+  if (G1 || !have_n) wait_vmcnt<0>();
 
   if constexpr (G1) {
     // SwiGLU (kernel.py:126-129) and 1x128 requantisation (kernel.py:131-135 with 128
     // columns): the tile's 128 columns are one scale block, spread over the 4 wavefronts
-    // that share this wave's item rows. Their row amax meet in the weight tile of stage
-    // kAmaxStage, which no wave reads or loads any more.
-    float(*amax_buf)[ROWS] = reinterpret_cast<float(*)[ROWS]>(sh.st[kAmaxStage].w);
-    // every wave's loads (the last two steps reload the last step into two stages, one of
-    // them kAmaxStage) have landed
+    // that share this wave's item rows. Their row amax meet in the weight tile of the stage
+    // of the unit's last step, which no load targets until the next unit's first step; the
+    // barrier shows that every wave is done reading it.
+    float(*amax_buf)[ROWS] = reinterpret_cast<float(*)[ROWS]>(sh.st[(s_base + KS - 1) % kStages].w);
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __builtin_amdgcn_s_barrier();
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
@@ -339,91 +351,121 @@ __device__ __forceinline__ void tile_body(const GemmParams& p, const TileCtx<ROW
 
 // NG (row groups of this wave's half) as a template argument: instantiations 0..kMaxNG.
 template <bool G1, int ROWS, int NG = 0>
-__device__ __forceinline__ void tile_body_ng(const GemmParams& p, const TileCtx<ROWS>& c, TileShared<ROWS>& sh, int ng) {
+__device__ __forceinline__ void tile_body_ng(const GemmParams& p, const TileCtx<ROWS>& c, const TileCtx<ROWS>& n,
+                                             bool have_n, int s_base, bool pre, TileShared<ROWS>& sh) {
   if constexpr (NG < TileShape<ROWS>::kMaxNG) {
-    if (ng == NG) tile_body<G1, NG, ROWS>(p, c, sh);
-    else tile_body_ng<G1, ROWS, NG + 1>(p, c, sh, ng);
+    if (c.ng == NG) tile_body<G1, NG, ROWS>(p, c, n, have_n, s_base, pre, sh);
+    else tile_body_ng<G1, ROWS, NG + 1>(p, c, n, have_n, s_base, pre, sh);
   } else {
-    tile_body<G1, NG, ROWS>(p, c, sh);
+    tile_body<G1, NG, ROWS>(p, c, n, have_n, s_base, pre, sh);
   }
+}
+
+// The pointers and item of work unit u for this lane (all of it wave-uniform but the DMA
+// offsets and the lane's block scales).
+template <bool G1, int ROWS>
+__device__ __forceinline__ void unit_setup(const GemmParams& p, int u, TileCtx<ROWS>& c) {
+  using S = TileShape<ROWS>;
+  constexpr int TILES = (G1 ? 2 * kInter : kHidden) / kTileW;
+  constexpr int KS = G1 ? kHBlocks : kIBlocks;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int q = u / TILES;
+  const int qw = reinterpret_cast<const int4*>(p.work_items)[q].w;
+  const int first = qw & 0xFFFF, ne = qw >> 16;
+  const int v = u - first * TILES;
+  const int4 it = reinterpret_cast<const int4*>(p.work_items)[first + v % ne];
+  // work-item fields are wave-uniform; say so, so that everything derived from them
+  // (notably the weight block-scale addresses) stays in scalar registers
+  const int e = __builtin_amdgcn_readfirstlane(it.x);
+  c.r0 = __builtin_amdgcn_readfirstlane(it.y);
+  c.rows = __builtin_amdgcn_readfirstlane(it.z);
+  c.tile = __builtin_amdgcn_readfirstlane(v / ne);
+
+  c.wbase = G1 ? p.w13 : p.w2;
+  // DMA j of this wave fills 8 tile rows, lane l writing row +l/8, physical chunk l%8
+  // (activation rows past the item's end repeat its first row)
+#pragma unroll
+  for (int j = 0; j < kWDma; ++j) {
+    const int r = 32 * wave + 8 * j + (lane >> 3);
+    const int ch = (lane & 7) ^ ((r >> 1) & 7);
+    size_t grow;
+    if constexpr (G1) grow = (size_t)e * 2 * kInter + (r < 128 ? c.tile * 128 + r : kInter + c.tile * 128 + r - 128);
+    else grow = (size_t)e * kHidden + c.tile * kTileW + r;
+    c.woff[j] = (uint32_t)(grow * (G1 ? kHidden : kInter) + ch * 16);
+  }
+  // activation DMA j of this wave fills tile rows 8i .. 8i+7 with i = wave + 8j (j = 2 for
+  // waves 0-3 of the 160-row tile only; otherwise unused)
+#pragma unroll
+  for (int j = 0; j < 3; ++j) {
+    const int blk = min(wave + kTileWaves * j, S::kABlocks - 1);
+    const int m = 8 * blk + (lane >> 3);
+    const int mm = m < c.rows ? m : 0;
+    const int ch = (lane & 7) ^ ((m >> 1) & 7);
+    size_t row;
+    if constexpr (G1) row = (size_t)p.sorted_token[c.r0 + mm] * kHidden;
+    else row = (size_t)(c.r0 + mm) * kInter;
+    c.asrc[j] = (G1 ? p.hidden : p.act) + row + ch * 16;
+  }
+  {
+    // the wave's 64-row block of scales: w % 4 (128 rows) or w - 4 (160 rows, waves 4-7),
+    // capped at the last block
+    c.sblk = min(S::kThirdBlock ? max(wave - 4, 0) : (wave & 3), S::kSBlocks - 1);
+    const int m = 64 * c.sblk + lane;
+    const int mm = m < c.rows ? m : 0;
+    if constexpr (G1) c.ssrc = p.hidden_scale + p.sorted_token[c.r0 + mm];
+    else c.ssrc = p.act_scale + (size_t)(c.r0 + mm) * kIBlocks;
+    c.sstride = G1 ? (size_t)p.T : 1;
+  }
+  const float* swp0;
+  const float* swp1;
+  if constexpr (G1) {
+    swp0 = p.w13_scale + ((size_t)e * 32 + c.tile) * kHBlocks;
+    swp1 = p.w13_scale + ((size_t)e * 32 + kIBlocks + c.tile) * kHBlocks;
+  } else {
+    swp0 = p.w2_scale + ((size_t)e * kHBlocks + (c.tile * kTileW + 64 * (wave & 3)) / 128) * kIBlocks;
+    swp1 = swp0;
+  }
+  c.sw0_lane = swp0[lane < KS ? lane : 0];
+  c.sw1_lane = swp1[lane < KS ? lane : 0];
+  // the item's row groups, split between the two wavefront halves (half 0 takes the odd one)
+  const int groups = (c.rows + 15) >> 4;
+  const int g0 = (groups + 1) >> 1;
+  c.ng = (wave >> 2) == 0 ? g0 : groups - g0;
+  c.m0 = (wave >> 2) == 0 ? 0 : 16 * g0;
 }
 
 template <bool G1, int ROWS>
 __global__ __launch_bounds__(kTileWaves * 64, 1) void gemm_tile_kernel(GemmParams p) {
-  using S = TileShape<ROWS>;
   constexpr int TILES = (G1 ? 2 * kInter : kHidden) / kTileW;
+  constexpr int KS = G1 ? kHBlocks : kIBlocks;
   __shared__ __attribute__((aligned(1024))) TileShared<ROWS> sh;
 
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n_items = min(p.counters[kCtrItems], p.max_items);
   const int units = n_items * TILES;
   const int per_xcd = (units + 7) >> 3;
-
-  for (int w = blockIdx.x; w < 8 * per_xcd; w += gridDim.x) {
-    const int u = (w & 7) * per_xcd + (w >> 3);
-    if (u >= units) continue;
-    const int q = u / TILES;
-    const int qw = reinterpret_cast<const int4*>(p.work_items)[q].w;
-    const int first = qw & 0xFFFF, ne = qw >> 16;
-    const int v = u - first * TILES;
-    const int4 it = reinterpret_cast<const int4*>(p.work_items)[first + v % ne];
-    // work-item fields are wave-uniform; say so, so that everything derived from them
-    // (notably the weight block-scale addresses) stays in scalar registers
-    const int e = __builtin_amdgcn_readfirstlane(it.x);
-    TileCtx<ROWS> c;
-    c.r0 = __builtin_amdgcn_readfirstlane(it.y);
-    c.rows = __builtin_amdgcn_readfirstlane(it.z);
-    c.tile = __builtin_amdgcn_readfirstlane(v / ne);
-
-    c.wbase = G1 ? p.w13 : p.w2;
-    // DMA j of this wave fills 8 tile rows, lane l writing row +l/8, physical chunk l%8
-    // (activation rows past the item's end repeat its first row)
-#pragma unroll
-    for (int j = 0; j < kWDma; ++j) {
-      const int r = 32 * wave + 8 * j + (lane >> 3);
-      const int ch = (lane & 7) ^ ((r >> 1) & 7);
-      size_t grow;
-      if constexpr (G1) grow = (size_t)e * 2 * kInter + (r < 128 ? c.tile * 128 + r : kInter + c.tile * 128 + r - 128);
-      else grow = (size_t)e * kHidden + c.tile * kTileW + r;
-      c.woff[j] = (uint32_t)(grow * (G1 ? kHidden : kInter) + ch * 16);
-    }
-    // activation DMA j of this wave fills tile rows 8i .. 8i+7 with i = wave + 8j (j = 2 for
-    // waves 0-3 of the 160-row tile only; otherwise unused)
-#pragma unroll
-    for (int j = 0; j < 3; ++j) {
-      const int blk = min(wave + kTileWaves * j, S::kABlocks - 1);
-      const int m = 8 * blk + (lane >> 3);
-      const int mm = m < c.rows ? m : 0;
-      const int ch = (lane & 7) ^ ((m >> 1) & 7);
-      size_t row;
-      if constexpr (G1) row = (size_t)p.sorted_token[c.r0 + mm] * kHidden;
-      else row = (size_t)(c.r0 + mm) * kInter;
-      c.asrc[j] = (G1 ? p.hidden : p.act) + row + ch * 16;
-    }
-    {
-      // the wave's 64-row block of scales: w % 4 (128 rows) or w - 4 (160 rows, waves 4-7),
-      // capped at the last block
-      c.sblk = min(S::kThirdBlock ? max(wave - 4, 0) : (wave & 3), S::kSBlocks - 1);
-      const int m = 64 * c.sblk + lane;
-      const int mm = m < c.rows ? m : 0;
-      if constexpr (G1) c.ssrc = p.hidden_scale + p.sorted_token[c.r0 + mm];
-      else c.ssrc = p.act_scale + (size_t)(c.r0 + mm) * kIBlocks;
-      c.sstride = G1 ? (size_t)p.T : 1;
-    }
-    if constexpr (G1) {
-      c.swp0 = p.w13_scale + ((size_t)e * 32 + c.tile) * kHBlocks;
-      c.swp1 = p.w13_scale + ((size_t)e * 32 + kIBlocks + c.tile) * kHBlocks;
-    } else {
-      c.swp0 = p.w2_scale + ((size_t)e * kHBlocks + (c.tile * kTileW + 64 * (wave & 3)) / 128) * kIBlocks;
-      c.swp1 = c.swp0;
-    }
-    // the item's row groups, split between the two wavefront halves (half 0 takes the odd one)
-    const int groups = (c.rows + 15) >> 4;
-    const int g0 = (groups + 1) >> 1;
-    const int ng = (wave >> 2) == 0 ? g0 : groups - g0;
-    c.m0 = (wave >> 2) == 0 ? 0 : 16 * g0;
-    tile_body_ng<G1, ROWS>(p, c, sh, ng);
+  // slot w of the static schedule: unit (w % 8) * per_xcd + w / 8 (consecutive slots go to
+  // different XCDs, each XCD's units are one contiguous range); a work-group takes slots
+  // blockIdx.x, + gridDim.x, .. (a multiple of 8: always the same XCD), and once a slot's unit
+  // is past the end so are all its later ones
+  auto unit_of = [&](int w) { return (w & 7) * per_xcd + (w >> 3); };
+  int w = blockIdx.x;
+  if (w >= 8 * per_xcd || unit_of(w) >= units) return;
+  TileCtx<ROWS> c, n;
+  unit_setup<G1, ROWS>(p, unit_of(w), c);
+  int s_base = 0;
+  bool pre = false;
+  for (;;) {
+    const int wn = w + gridDim.x;
+    const bool have_n = wn < 8 * per_xcd && unit_of(wn) < units;
+    if (have_n) unit_setup<G1, ROWS>(p, unit_of(wn), n);
+    else n = c;
+    tile_body_ng<G1, ROWS>(p, c, n, have_n, s_base, pre, sh);
+    if (!have_n) break;
+    w = wn;
+    c = n;
+    s_base = (s_base + KS) % kStages;
+    pre = !G1;
   }
 }
 
