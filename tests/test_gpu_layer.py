@@ -184,15 +184,27 @@ def _given_topk(case, T, rng):
     elif case == "repeat":                       # a token naming one local expert twice
         ids[:, 0] = rng.integers(0, 32, size=T)
         ids[:, 1] = ids[:, 0]
+    elif case == "few_local":
+        # large-T items of every shape: expert 5 with 300 rows (two items), expert 17 with
+        # exactly 160 (one full item), expert 9 with 200 (two), expert 30 with 20; tokens
+        # 0..39 have two local experts (combined), tokens from 640 on none
+        ids = np.where(ids < 32, ids + 32, ids)
+        ids[0:300, 0] = 5
+        ids[300:460, 0] = 9
+        ids[460:480, 0] = 30
+        ids[480:640, 0] = 17
+        ids[0:40, 1] = 9
     w = (rng.random((T, 8)) * 0.5 + 0.1).astype(np.float32)
     return ids, w
 
 
 @pytest.mark.parametrize("T,case", [(1, "all_local"), (40, "repeat"), (300, "all_local"),
-                                    (600, "one_expert"), (600, "none_local")])
+                                    (600, "one_expert"), (600, "none_local"), (4100, "few_local")])
 def test_layer_edge_cases_given_topk(T, case):
     """The GEMM stages on constructed top-k lists: one token, a repeated expert, every token
-    on one expert (many items of one expert on the tile path), nothing local."""
+    on one expert (many items of one expert on the tile path), nothing local, and at T >= 4096
+    (items of up to 160 rows) items of every shape next to thousands of tokens without a
+    local expert."""
     gh = _gh()
     dev = torch.device("cuda:0")
     w, wnp = _weights()
@@ -217,12 +229,17 @@ def test_layer_edge_cases_given_topk(T, case):
     npkw = gh.to_numpy_inputs({**kw, "gemm1_weights": w[0][:1], "gemm2_weights": w[2][:1]})
     npkw["gemm1_weights"], npkw["gemm1_weights_scale"], npkw["gemm2_weights"], npkw["gemm2_weights_scale"] = wnp
     tokens = None if T <= 40 else np.sort(rng.choice(T, 24, replace=False))
+    if case == "few_local":   # every kind of token: 2 local experts, each item's edges, none
+        tokens = np.unique(np.concatenate([tokens, [0, 39, 40, 299, 300, 459, 460, 479, 480, 639, 640, T - 1]]))
     emu = olayer.layer_forward(**npkw, mode="emulated", topk=(ids, tw), tokens=tokens)
     sel = slice(None) if tokens is None else tokens
     if case == "none_local":
         assert np.all(got == 0)
         return
     _compare(got[sel], emu["output"], 0.02, 0.02, 0.01, f"T={T} {case} vs emulated oracle")
+    if case == "few_local":
+        assert ws.layout.rows_per_item == 160
+        assert np.all(got[640:] == 0)
 
 
 def test_layer_last_expert_group():
