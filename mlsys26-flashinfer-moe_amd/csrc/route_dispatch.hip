@@ -442,7 +442,11 @@ __global__ __launch_bounds__(kRouteThreads) void dispatch_small_kernel(RoutePara
 }
 
 // Large batches, step 2 (one work-group): per-expert exclusive prefix of the work-group
-// histograms (in place), CSR offsets and the work list.
+// histograms (in place), CSR offsets and the work list. Thread (j, e) owns a run of the
+// work-groups for expert e; it reads their counts kScanBatch at a time, all loads of a batch
+// in flight together (a load-then-add loop would wait out one memory latency per count).
+constexpr int kScanBatch = 16;
+
 __global__ __launch_bounds__(kRouteThreads) void scan_kernel(RouteParams p) {
   __shared__ int s_part[32][kExpertsLocal];
   __shared__ int s_start[kExpertsLocal + 1];
@@ -452,7 +456,13 @@ __global__ __launch_bounds__(kRouteThreads) void scan_kernel(RouteParams p) {
   const int chunk = (nb + 31) / 32;
   const int b0 = min(nb, j * chunk), b1 = min(nb, b0 + chunk);
   int sum = 0;
-  for (int b = b0; b < b1; ++b) sum += p.block_count[b * kExpertsLocal + e];
+  for (int bb = b0; bb < b1; bb += kScanBatch) {
+    int v[kScanBatch];
+#pragma unroll
+    for (int i = 0; i < kScanBatch; ++i) v[i] = bb + i < b1 ? p.block_count[(bb + i) * kExpertsLocal + e] : 0;
+#pragma unroll
+    for (int i = 0; i < kScanBatch; ++i) sum += v[i];
+  }
   s_part[j][e] = sum;
   __syncthreads();
   if (tid < kExpertsLocal) {
@@ -466,10 +476,15 @@ __global__ __launch_bounds__(kRouteThreads) void scan_kernel(RouteParams p) {
   }
   __syncthreads();
   int run = s_part[j][e];
-  for (int b = b0; b < b1; ++b) {
-    const int v = p.block_count[b * kExpertsLocal + e];
-    p.block_count[b * kExpertsLocal + e] = run;
-    run += v;
+  for (int bb = b0; bb < b1; bb += kScanBatch) {
+    int v[kScanBatch];
+#pragma unroll
+    for (int i = 0; i < kScanBatch; ++i) v[i] = bb + i < b1 ? p.block_count[(bb + i) * kExpertsLocal + e] : 0;
+#pragma unroll
+    for (int i = 0; i < kScanBatch; ++i) {
+      if (bb + i < b1) p.block_count[(bb + i) * kExpertsLocal + e] = run;
+      run += v[i];
+    }
   }
 }
 
