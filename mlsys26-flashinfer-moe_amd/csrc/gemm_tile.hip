@@ -32,9 +32,18 @@
 // LDS tiles: 16-byte chunk c of row m lives at m*128 + ((c ^ ((m >> 1) & 7)) * 16), which
 // spreads the 16 rows read by one ds_read_b128 across distinct bank groups.
 //
-// Scheduling: the work units (item, tile) of expert e are numbered tile-major
-// (all items of one weight tile are consecutive) and dealt to the 8 XCDs in contiguous
-// blocks, so the items sharing a weight tile run together on one XCD and reuse it from L2.
+// Scheduling: the work units (item, tile) of expert e are numbered tile-major (all items of
+// one weight tile are consecutive); the items sharing a weight tile run together on one XCD
+// and reuse it from L2.
+//   GEMM1: XCD x takes weight tiles t0, t0 + 8 of every expert, t0 = (x - 4 * (rank % 2)) % 8
+//          for the expert's rank by descending item rows, so that every XCD gets the same
+//          mix of long and short units; its work-groups take the units of that list, longest
+//          experts first, from a per-XCD counter as they finish (measured against contiguous
+//          blocks of units per XCD: GEMM1 296 against 313 us at T=8192, 164 against 174 at
+//          T=1024, 656 against 682 on the skewed T=4096 batch).
+//   GEMM2: the units are dealt to the 8 XCDs in contiguous blocks, a work-group's units
+//          fixed in advance, so that a unit can prefetch the next one's first K-steps (the
+//          per-XCD lists above measured slower here without that prefetch).
 #include "moe_internal.h"
 #include "moe_device.h"
 
@@ -92,9 +101,13 @@ struct TileStage {
   float sa[TileShape<ROWS>::kSSlots];   // scale of item row m at m
 };
 
+// The ring and GEMM1's next list entry share one LDS object: with a second __shared__
+// variable the compiler no longer tells the ring's DMA writes from its reads and waits for
+// every load in flight before each LDS read.
 template <int ROWS>
 struct TileShared {
   TileStage<ROWS> st[kStages];
+  int next;
 };
 static_assert(sizeof(TileShared<kTileItemRowsLarge>) <= 160 * 1024, "LDS of one CU");
 static_assert(4 * kTileItemRowsLarge * sizeof(float) <= kTileW * 128, "amax fits in a weight tile");
@@ -128,7 +141,8 @@ __device__ __forceinline__ v8i lds_frag(const uint8_t* buf, int m, int lane) {
 // steps, like GEMM2's last unit's, load the last step again into stages nobody reads.
 template <bool G1, int NG, int ROWS>
 __device__ __forceinline__ void tile_body(const GemmParams& p, const TileCtx<ROWS>& c, const TileCtx<ROWS>& n,
-                                          bool have_n, int s_base, bool pre, TileShared<ROWS>& sh) {
+                                          bool have_n, int s_base, bool pre, TileShared<ROWS>& sh,
+                                          int32_t* queue) {
   using S = TileShape<ROWS>;
   constexpr int KS = G1 ? kHBlocks : kIBlocks;
   const int lane = threadIdx.x & 63;
@@ -277,6 +291,11 @@ __device__ __forceinline__ void tile_body(const GemmParams& p, const TileCtx<ROW
   // The loads in flight now are the next unit's first two steps, or reloads nobody reads; the
   // reloads must land before the next unit refills the ring.
   if (G1 || !have_n) wait_vmcnt<0>();
+  // GEMM1: the work-group's next list entry; the counter's round trip overlaps the epilogue
+  int got = 0;
+  if constexpr (G1) {
+    if (threadIdx.x == 0) got = atomicAdd(queue, 1);
+  }
 
   if constexpr (G1) {
     // SwiGLU (kernel.py:126-129) and 1x128 requantisation (kernel.py:131-135 with 128
@@ -347,17 +366,21 @@ __device__ __forceinline__ void tile_body(const GemmParams& p, const TileCtx<ROW
       }
     }
   }
+  if constexpr (G1) {
+    if (threadIdx.x == 0) sh.next = got;
+  }
 }
 
 // NG (row groups of this wave's half) as a template argument: instantiations 0..kMaxNG.
 template <bool G1, int ROWS, int NG = 0>
 __device__ __forceinline__ void tile_body_ng(const GemmParams& p, const TileCtx<ROWS>& c, const TileCtx<ROWS>& n,
-                                             bool have_n, int s_base, bool pre, TileShared<ROWS>& sh) {
+                                             bool have_n, int s_base, bool pre, TileShared<ROWS>& sh,
+                                             int32_t* queue) {
   if constexpr (NG < TileShape<ROWS>::kMaxNG) {
-    if (c.ng == NG) tile_body<G1, NG, ROWS>(p, c, n, have_n, s_base, pre, sh);
-    else tile_body_ng<G1, ROWS, NG + 1>(p, c, n, have_n, s_base, pre, sh);
+    if (c.ng == NG) tile_body<G1, NG, ROWS>(p, c, n, have_n, s_base, pre, sh, queue);
+    else tile_body_ng<G1, ROWS, NG + 1>(p, c, n, have_n, s_base, pre, sh, queue);
   } else {
-    tile_body<G1, NG, ROWS>(p, c, n, have_n, s_base, pre, sh);
+    tile_body<G1, NG, ROWS>(p, c, n, have_n, s_base, pre, sh, queue);
   }
 }
 
@@ -435,6 +458,51 @@ __device__ __forceinline__ void unit_setup(const GemmParams& p, int u, TileCtx<R
   c.m0 = (wave >> 2) == 0 ? 0 : 16 * g0;
 }
 
+// GEMM1's per-XCD work list (see the top of the file). Lane k < 32 of every wavefront holds
+// the k-th expert of the order the dispatch recorded: its first item, item count, first weight
+// tile on this XCD and the list position of its first unit.
+template <int TILES>
+struct XcdList {
+  int first, ne, t0, pos;
+  int total;   // entries of the list (wave-uniform)
+
+  // Work unit of list entry j; false past the end. j must be wave-uniform.
+  __device__ __forceinline__ bool entry(int j, int& u) const {
+    if (j >= total) return false;
+    const int lane = threadIdx.x & 63;
+    // the last expert that starts at or before j (experts with units come first)
+    const unsigned long long m = __ballot(lane < kExpertsLocal && ne > 0 && pos <= j);
+    const int k = 63 - __builtin_clzll(m);
+    const int ne_k = __builtin_amdgcn_readlane(ne, k);
+    const int r = j - __builtin_amdgcn_readlane(pos, k);
+    const int ti = r / ne_k;
+    const int tile = __builtin_amdgcn_readlane(t0, k) + 8 * ti;
+    u = __builtin_amdgcn_readlane(first, k) * TILES + tile * ne_k + (r - ti * ne_k);
+    return true;
+  }
+};
+
+template <int TILES>
+__device__ __forceinline__ XcdList<TILES> xcd_list(const GemmParams& p, int x, int n_items) {
+  XcdList<TILES> l;
+  const int lane = threadIdx.x & 63;
+  const int ord = lane < kExpertsLocal ? p.counters[kCtrOrder + lane] : 0;
+  l.first = ord & 0xFFFF;
+  l.ne = ord >> 16;
+  if (l.first + l.ne > n_items) l.ne = 0;
+  l.t0 = (x - 4 * (lane & 1)) & 7;
+  const int len = ((TILES - l.t0 + 7) >> 3) * l.ne;
+  int incl = len;
+#pragma unroll
+  for (int off = 1; off < kExpertsLocal; off <<= 1) {
+    const int o = __shfl_up(incl, off);
+    if (lane >= off) incl += o;
+  }
+  l.pos = incl - len;
+  l.total = __builtin_amdgcn_readfirstlane(__shfl(incl, kExpertsLocal - 1));
+  return l;
+}
+
 template <bool G1, int ROWS>
 __global__ __launch_bounds__(kTileWaves * 64, 1) void gemm_tile_kernel(GemmParams p) {
   constexpr int TILES = (G1 ? 2 * kInter : kHidden) / kTileW;
@@ -442,30 +510,64 @@ __global__ __launch_bounds__(kTileWaves * 64, 1) void gemm_tile_kernel(GemmParam
   __shared__ __attribute__((aligned(1024))) TileShared<ROWS> sh;
 
   const int n_items = min(p.counters[kCtrItems], p.max_items);
-  const int units = n_items * TILES;
-  const int per_xcd = (units + 7) >> 3;
-  // slot w of the static schedule: unit (w % 8) * per_xcd + w / 8 (consecutive slots go to
-  // different XCDs, each XCD's units are one contiguous range); a work-group takes slots
-  // blockIdx.x, + gridDim.x, .. (a multiple of 8: always the same XCD), and once a slot's unit
-  // is past the end so are all its later ones
-  auto unit_of = [&](int w) { return (w & 7) * per_xcd + (w >> 3); };
-  int w = blockIdx.x;
-  if (w >= 8 * per_xcd || unit_of(w) >= units) return;
-  TileCtx<ROWS> c, n;
-  unit_setup<G1, ROWS>(p, unit_of(w), c);
-  int s_base = 0;
-  bool pre = false;
-  for (;;) {
-    const int wn = w + gridDim.x;
-    const bool have_n = wn < 8 * per_xcd && unit_of(wn) < units;
-    if (have_n) unit_setup<G1, ROWS>(p, unit_of(wn), n);
-    else n = c;
-    tile_body_ng<G1, ROWS>(p, c, n, have_n, s_base, pre, sh);
-    if (!have_n) break;
-    w = wn;
-    c = n;
-    s_base = (s_base + KS) % kStages;
-    pre = !G1;
+  if constexpr (G1) {
+    // XCD x = blockIdx.x % 8 (the grid is a multiple of 8): a work-group starts on list entry
+    // blockIdx.x / 8 and takes each later one from the XCD's counter (restarted by the
+    // dispatch), offset by the work-groups per XCD. All waves of a work-group see the same
+    // entries, so all leave together.
+    const int x = blockIdx.x & 7;
+    const XcdList<TILES> list = xcd_list<TILES>(p, x, n_items);
+    int32_t* queue = p.counters + kCtrQueue + x;
+    const int per_xcd = gridDim.x >> 3;
+    int u;
+    if (list.entry(blockIdx.x >> 3, u)) {
+      TileCtx<ROWS> c;
+      unit_setup<G1, ROWS>(p, u, c);
+      int s_base = 0;
+      for (;;) {
+        tile_body_ng<G1, ROWS>(p, c, c, false, s_base, false, sh, queue);
+        __syncthreads();
+        if (!list.entry(per_xcd + __builtin_amdgcn_readfirstlane(sh.next), u)) break;
+        unit_setup<G1, ROWS>(p, u, c);
+        s_base = (s_base + KS) % kStages;
+      }
+    }
+    // The XCD's last work-group to leave restarts its counters, so that a launch of this
+    // stage alone finds them at zero too: every other work-group's last entry has returned
+    // before it counted itself out.
+    if (threadIdx.x == 0) {
+      int32_t* left = p.counters + kCtrLeft + x;
+      if (atomicAdd(left, 1) == per_xcd - 1) {
+        atomicExch(queue, 0);
+        atomicExch(left, 0);
+      }
+    }
+  } else {
+    const int units = n_items * TILES;
+    const int per_xcd = (units + 7) >> 3;
+    // slot w of the static schedule: unit (w % 8) * per_xcd + w / 8 (consecutive slots go to
+    // different XCDs, each XCD's units are one contiguous range); a work-group takes slots
+    // blockIdx.x, + gridDim.x, .. (a multiple of 8: always the same XCD), and once a slot's
+    // unit is past the end so are all its later ones
+    auto unit_of = [&](int w) { return (w & 7) * per_xcd + (w >> 3); };
+    int w = blockIdx.x;
+    if (w >= 8 * per_xcd || unit_of(w) >= units) return;
+    TileCtx<ROWS> c, n;
+    unit_setup<G1, ROWS>(p, unit_of(w), c);
+    int s_base = 0;
+    bool pre = false;
+    for (;;) {
+      const int wn = w + gridDim.x;
+      const bool have_n = wn < 8 * per_xcd && unit_of(wn) < units;
+      if (have_n) unit_setup<G1, ROWS>(p, unit_of(wn), n);
+      else n = c;
+      tile_body_ng<G1, ROWS>(p, c, n, have_n, s_base, pre, sh, nullptr);
+      if (!have_n) break;
+      w = wn;
+      c = n;
+      s_base = (s_base + KS) % kStages;
+      pre = true;
+    }
   }
 }
 

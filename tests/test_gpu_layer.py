@@ -153,6 +153,31 @@ def test_intermediate_fp8_matches_oracle(name):
     assert np.all(err <= bound)
 
 
+@pytest.mark.parametrize("name", ["t1024_off64", "t4096_skew"])
+def test_tile_stage_repeated(name):
+    """The GEMM1 tile kernel takes its units from per-XCD counters that the dispatch restarts.
+    GEMM1 launched again after its result was wiped (no dispatch in between) redoes every unit:
+    the launch before left the counters restarted. Staged and whole-layer runs agree bitwise."""
+    gh = _gh()
+    kw, _ = _workload(name)
+    T = kw["routing_logits"].shape[0]
+    print(f"tile stage repeated {name} T={T}", flush=True)
+    whole = _run_full(kw)
+    dev = kw["routing_logits"].device
+    out = torch.full((T, 7168), float("nan"), dtype=torch.bfloat16, device=dev)
+    ws = gh.new_workspace(T, dev)
+    assert ws.layout.rows_per_item > 32
+    args = gh.make_args(**kw, output=out)
+    gh.route_dispatch(args, ws)
+    gh.gemm1(args, ws)
+    n = int(gh.counters(ws)[1])
+    gh.write(ws, "act", np.zeros(n * 2048, dtype=np.uint8))
+    gh.gemm1(args, ws)
+    gh.gemm2_combine(args, ws)
+    torch.cuda.synchronize()
+    assert torch.equal(whole.view(torch.int16), out.view(torch.int16)), "staged and whole-layer runs differ"
+
+
 def test_deterministic_and_fp32_output():
     kw, npkw = _workload("t1024_off64")
     a = _run_full(kw)
