@@ -35,15 +35,18 @@
 // Scheduling: the work units (item, tile) of expert e are numbered tile-major (all items of
 // one weight tile are consecutive); the items sharing a weight tile run together on one XCD
 // and reuse it from L2.
-//   GEMM1: XCD x takes weight tiles t0, t0 + 8 of every expert, t0 = (x - 4 * (rank % 2)) % 8
-//          for the expert's rank by descending item rows, so that every XCD gets the same
-//          mix of long and short units; its work-groups take the units of that list, longest
-//          experts first, from a per-XCD counter as they finish (measured against contiguous
-//          blocks of units per XCD: GEMM1 296 against 313 us at T=8192, 164 against 174 at
-//          T=1024, 656 against 682 on the skewed T=4096 batch).
-//   GEMM2: the units are dealt to the 8 XCDs in contiguous blocks, a work-group's units
-//          fixed in advance, so that a unit can prefetch the next one's first K-steps (the
-//          per-XCD lists above measured slower here without that prefetch).
+//   Per-XCD lists (GEMM1; GEMM2 with items of up to 128 rows): XCD x takes weight tiles
+//          t0, t0 + 8, .. of every expert, t0 = (x - 4 * (rank % 2)) % 8 for the expert's rank
+//          by descending item rows, so that every XCD gets the same mix of long and short
+//          units; its work-groups take the units of that list, longest experts first, from a
+//          per-XCD counter as they finish. GEMM2 reserves one entry ahead, so that a unit
+//          knows the next one in time to prefetch its first K-steps. Measured against
+//          contiguous blocks of units per XCD: GEMM1 296 against 313 us at T=8192, 164
+//          against 174 at T=1024, 656 against 682 on the skewed T=4096 batch; GEMM2 +
+//          combine 114 against 123 us at T=1024.
+//   Static blocks (GEMM2 with items of up to 160 rows): the units are dealt to the 8 XCDs in
+//          contiguous blocks, a work-group's units fixed in advance (the lists measured 253
+//          against 247 us at T=8192 and 573 against 552 on the skewed batch).
 #include "moe_internal.h"
 #include "moe_device.h"
 
@@ -101,7 +104,7 @@ struct TileStage {
   float sa[TileShape<ROWS>::kSSlots];   // scale of item row m at m
 };
 
-// The ring and GEMM1's next list entry share one LDS object: with a second __shared__
+// The ring and the next list entry share one LDS object: with a second __shared__
 // variable the compiler no longer tells the ring's DMA writes from its reads and waits for
 // every load in flight before each LDS read.
 template <int ROWS>
@@ -291,11 +294,10 @@ __device__ __forceinline__ void tile_body(const GemmParams& p, const TileCtx<ROW
   // The loads in flight now are the next unit's first two steps, or reloads nobody reads; the
   // reloads must land before the next unit refills the ring.
   if (G1 || !have_n) wait_vmcnt<0>();
-  // GEMM1: the work-group's next list entry; the counter's round trip overlaps the epilogue
+  // the work-group's next list entry (per-XCD lists); the counter's round trip overlaps the
+  // epilogue
   int got = 0;
-  if constexpr (G1) {
-    if (threadIdx.x == 0) got = atomicAdd(queue, 1);
-  }
+  if (queue != nullptr && threadIdx.x == 0) got = atomicAdd(queue, 1);
 
   if constexpr (G1) {
     // SwiGLU (kernel.py:126-129) and 1x128 requantisation (kernel.py:131-135 with 128
@@ -366,9 +368,7 @@ __device__ __forceinline__ void tile_body(const GemmParams& p, const TileCtx<ROW
       }
     }
   }
-  if constexpr (G1) {
-    if (threadIdx.x == 0) sh.next = got;
-  }
+  if (queue != nullptr && threadIdx.x == 0) sh.next = got;
 }
 
 // NG (row groups of this wave's half) as a template argument: instantiations 0..kMaxNG.
@@ -458,7 +458,7 @@ __device__ __forceinline__ void unit_setup(const GemmParams& p, int u, TileCtx<R
   c.m0 = (wave >> 2) == 0 ? 0 : 16 * g0;
 }
 
-// GEMM1's per-XCD work list (see the top of the file). Lane k < 32 of every wavefront holds
+// A per-XCD work list (see the top of the file). Lane k < 32 of every wavefront holds
 // the k-th expert of the order the dispatch recorded: its first item, item count, first weight
 // tile on this XCD and the list position of its first unit.
 template <int TILES>
@@ -510,25 +510,40 @@ __global__ __launch_bounds__(kTileWaves * 64, 1) void gemm_tile_kernel(GemmParam
   __shared__ __attribute__((aligned(1024))) TileShared<ROWS> sh;
 
   const int n_items = min(p.counters[kCtrItems], p.max_items);
-  if constexpr (G1) {
+  if constexpr (G1 || ROWS == kTileItemRowsMid) {
     // XCD x = blockIdx.x % 8 (the grid is a multiple of 8): a work-group starts on list entry
-    // blockIdx.x / 8 and takes each later one from the XCD's counter (restarted by the
-    // dispatch), offset by the work-groups per XCD. All waves of a work-group see the same
-    // entries, so all leave together.
+    // blockIdx.x / 8 (GEMM2: and reserves blockIdx.x / 8 + per_xcd) and takes each later one
+    // from the XCD's counter (restarted by the dispatch), offset by the entries handed out
+    // up front. All waves of a work-group see the same entries, so all leave together.
     const int x = blockIdx.x & 7;
     const XcdList<TILES> list = xcd_list<TILES>(p, x, n_items);
-    int32_t* queue = p.counters + kCtrQueue + x;
+    int32_t* queue = p.counters + kCtrQueue + (G1 ? 0 : 8) + x;
     const int per_xcd = gridDim.x >> 3;
     int u;
     if (list.entry(blockIdx.x >> 3, u)) {
-      TileCtx<ROWS> c;
+      TileCtx<ROWS> c, n;
       unit_setup<G1, ROWS>(p, u, c);
+      bool have_n = false;
+      if constexpr (!G1) have_n = list.entry(per_xcd + (blockIdx.x >> 3), u);
+      if (have_n) unit_setup<G1, ROWS>(p, u, n);
+      else n = c;
       int s_base = 0;
+      bool pre = false;
       for (;;) {
-        tile_body_ng<G1, ROWS>(p, c, c, false, s_base, false, sh, queue);
+        tile_body_ng<G1, ROWS>(p, c, n, have_n, s_base, pre, sh, queue);
         __syncthreads();
-        if (!list.entry(per_xcd + __builtin_amdgcn_readfirstlane(sh.next), u)) break;
-        unit_setup<G1, ROWS>(p, u, c);
+        const int j = (G1 ? 1 : 2) * per_xcd + __builtin_amdgcn_readfirstlane(sh.next);
+        if constexpr (G1) {
+          if (!list.entry(j, u)) break;
+          unit_setup<G1, ROWS>(p, u, c);
+        } else {
+          if (!have_n) break;
+          c = n;
+          have_n = list.entry(j, u);
+          if (have_n) unit_setup<G1, ROWS>(p, u, n);
+          else n = c;
+          pre = true;
+        }
         s_base = (s_base + KS) % kStages;
       }
     }
@@ -536,7 +551,7 @@ __global__ __launch_bounds__(kTileWaves * 64, 1) void gemm_tile_kernel(GemmParam
     // stage alone finds them at zero too: every other work-group's last entry has returned
     // before it counted itself out.
     if (threadIdx.x == 0) {
-      int32_t* left = p.counters + kCtrLeft + x;
+      int32_t* left = p.counters + kCtrLeft + (G1 ? 0 : 8) + x;
       if (atomicAdd(left, 1) == per_xcd - 1) {
         atomicExch(queue, 0);
         atomicExch(left, 0);

@@ -41,11 +41,11 @@ constexpr int kSinglePassTokens = 256;
 // Control block (workspace counters[]).
 constexpr int kCtrItems = 0;    // number of GEMM work items
 constexpr int kCtrAssign = 1;   // N, the number of local assignments
-constexpr int kCtrQueue = 8;    // [8] per-XCD unit counters of the GEMM1 tile kernel
-constexpr int kCtrLeft = 16;    // [8] its work-groups per XCD that have left
-constexpr int kCtrOrder = 32;   // [32] experts by descending item rows: first item | items << 16
-constexpr int kNumCounters = 64;
-static_assert(kCtrQueue + 8 <= kCtrLeft && kCtrLeft + 8 <= kCtrOrder && kCtrOrder + kExpertsLocal <= kNumCounters,
+constexpr int kCtrQueue = 16;   // [2][8] per-XCD unit counters of the GEMM1 and GEMM2 tile kernels
+constexpr int kCtrLeft = 32;    // [2][8] their work-groups per XCD that have left
+constexpr int kCtrOrder = 48;   // [32] experts by descending item rows: first item | items << 16
+constexpr int kNumCounters = 80;
+static_assert(kCtrQueue + 16 <= kCtrLeft && kCtrLeft + 16 <= kCtrOrder && kCtrOrder + kExpertsLocal <= kNumCounters,
               "control block");
 
 // Rows of a work item of the tile GEMMs: gemm_tile_kernel has an instance for items of up to
@@ -103,7 +103,7 @@ struct GemmParams {
   int T;
   int max_items;
   const int32_t* work_items;
-  int32_t* counters;           // read-only but for the GEMM1 tile kernel's unit counters
+  int32_t* counters;           // read-only but for the tile kernels' unit counters
   const int32_t* sorted_token;
   const float* sorted_weight;
   const int32_t* sorted_slot;

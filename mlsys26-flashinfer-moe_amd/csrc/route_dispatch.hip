@@ -272,8 +272,8 @@ __device__ __forceinline__ void finish_counts(const RouteParams& p, int e, int r
     reinterpret_cast<int4*>(p.work_items)[first + c] = it;
   }
   if (e == kExpertsLocal - 1) p.counters[kCtrItems] = ich;
-  // The order in which the GEMM1 tile kernel's per-XCD lists visit the experts: by descending
-  // item rows (ties by expert index), experts without rows last. Its unit counters restart.
+  // The order in which the tile kernels' per-XCD lists visit the experts: by descending item
+  // rows (ties by expert index), experts without rows last. Their unit counters restart.
   const int key = nch > 0 ? min(chunk, run) : 0;
   int rank = 0;
   for (int o = 0; o < kExpertsLocal; ++o) {
@@ -281,7 +281,7 @@ __device__ __forceinline__ void finish_counts(const RouteParams& p, int e, int r
     rank += (ko > key || (ko == key && o < e)) ? 1 : 0;
   }
   p.counters[kCtrOrder + rank] = first | (nch << 16);
-  if (e < 8) {
+  if (e < 16) {
     p.counters[kCtrQueue + e] = 0;
     p.counters[kCtrLeft + e] = 0;
   }
