@@ -107,7 +107,7 @@ typedef struct moe_fp8_args {
  *   work_items    int32 [max_items, 4]  GEMM work list (expert, first row, rows,
  *                                   first item of the expert | its item count << 16) (kernel.py:384-407)
  *   counters      int32 [80]        [0] number of work items, [1] N; the rest internal
- *                                   (the GEMM1 tile kernel's work-list state)
+ *                                   (the tile kernels' work-list state)
  *   act           fp8   [N_max, 2048]    SwiGLU output requantised to e4m3fn          (kernel.py:669)
  *   act_scale     fp32  [N_max, 16]      its 1x128 block scales, row-major per row   (kernel.py:670)
  *   partial       fp32  [T*8, 7168]      weighted GEMM2 rows of tokens with more than one local
