@@ -110,6 +110,14 @@ __device__ __forceinline__ void stream_unit(const GemmParams& p, int e, int r0, 
     for (int f = 0; f < NF; ++f) sw_lane[f] = sw;
   }
 
+  StreamStage<NF, NG> ring[NB];
+  // the weight loads of the first steps go out before the activation addresses are known
+  // (GEMM1 reads them from sorted_token, one more memory round trip)
+#pragma unroll
+  for (int s = 0; s < NB - 1; ++s)
+#pragma unroll
+    for (int f = 0; f < NF; ++f) ring[s].w[f] = load_frag(wf[f] + s * 128);
+
   // activation rows of this lane's column in each 16-row group (rows past the item's end
   // read its first row; their results are never stored)
   const uint8_t* ap[NG];
@@ -129,18 +137,20 @@ __device__ __forceinline__ void stream_unit(const GemmParams& p, int e, int r0, 
   }
   const size_t sa_stride = (KIND == kG1) ? (size_t)p.T : 1;
 
-  StreamStage<NF, NG> ring[NB];
-  auto issue = [&](int k, StreamStage<NF, NG>& st) {
-#pragma unroll
-    for (int f = 0; f < NF; ++f) st.w[f] = load_frag(wf[f] + k * 128);
+  auto issue_a = [&](int k, StreamStage<NF, NG>& st) {
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
       st.a[g] = load_frag(ap[g] + k * 128);
       st.sa[g] = sap[g][k * sa_stride];
     }
   };
+  auto issue = [&](int k, StreamStage<NF, NG>& st) {
 #pragma unroll
-  for (int s = 0; s < NB - 1; ++s) issue(s, ring[s]);
+    for (int f = 0; f < NF; ++f) st.w[f] = load_frag(wf[f] + k * 128);
+    issue_a(k, st);
+  };
+#pragma unroll
+  for (int s = 0; s < NB - 1; ++s) issue_a(s, ring[s]);
 
   v4f acc[NF][NG];
 #pragma unroll
