@@ -39,8 +39,8 @@ constexpr int kStreamWaves = 4;                      // wavefronts per work-grou
 // and depth of the register ring.
 //   GEMM1: a unit is 16 SwiGLU columns = their 16 gate rows + 16 up rows (2 fragments).
 //   GEMM2: a unit is 64 hidden rows (4 fragments).
-// GEMM1 uses a 3-slot ring (two K-steps in flight per wavefront, 132 VGPRs), GEMM2 a
-// 2-slot ring (136 VGPRs): three wavefronts per SIMD, so that at decode sizes every unit
+// GEMM1 uses a 3-slot ring (two K-steps in flight per wavefront, 130 registers with the
+// accumulators), GEMM2 a 2-slot ring (136 registers): three wavefronts per SIMD, so that at decode sizes every unit
 // has its own wavefront and the grid drains in one round (measured at T=64: GEMM1
 // 117 -> 109 us, GEMM2 64 -> 57 us against 4-slot rings and 32-row GEMM2 units).
 // Requantising GEMM1's fp32 rows inside GEMM2 instead of in requant_kernel was measured
