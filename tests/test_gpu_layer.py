@@ -4,7 +4,8 @@ Tolerances (bf16 output, compared as float32):
   vs the emulated oracle (same fp8 requantisation of the SwiGLU output as the kernels,
   1x128 blocks): |gpu - ref| <= 0.02 + 0.02 |ref| element-wise and relative RMS <= 0.01;
   the residual comes from fp32 summation order, which flips a few fp8 roundings of the
-  intermediate;
+  intermediate (for constructed top-k lists the 0.02 grows as sqrt(max local experts per
+  token / 2), since every local expert adds its own flips);
   vs the definition (fp32 intermediate, kernel.py's math without requantisation):
   |gpu - ref| <= 0.1 + 0.1 |ref| element-wise and relative RMS <= 0.05.
 The fp8 intermediate itself: its scales within 1e-5 relative, and at most 1 code step
@@ -224,12 +225,14 @@ def _given_topk(case, T, rng):
 
 
 @pytest.mark.parametrize("T,case", [(1, "all_local"), (40, "repeat"), (300, "all_local"),
-                                    (600, "one_expert"), (600, "none_local"), (4100, "few_local")])
+                                    (513, "all_local"), (600, "one_expert"), (600, "none_local"),
+                                    (4095, "all_local"), (4096, "all_local"), (4100, "few_local")])
 def test_layer_edge_cases_given_topk(T, case):
     """The GEMM stages on constructed top-k lists: one token, a repeated expert, every token
     on one expert (many items of one expert on the tile path), nothing local, and at T >= 4096
     (items of up to 160 rows) items of every shape next to thousands of tokens without a
-    local expert."""
+    local expert. T=513 is the first batch on the tile kernels; T=4095 and T=4096 put 1024 rows
+    on every local expert, the largest batch of 128-row items and the first of 160-row items."""
     gh = _gh()
     dev = torch.device("cuda:0")
     w, wnp = _weights()
@@ -261,7 +264,12 @@ def test_layer_edge_cases_given_topk(T, case):
     if case == "none_local":
         assert np.all(got == 0)
         return
-    _compare(got[sel], emu["output"], 0.02, 0.02, 0.01, f"T={T} {case} vs emulated oracle")
+    # Each output element sums one contribution per local expert, and each carries the fp8
+    # rounding flips of its intermediate; with up to 8 local experts per token the element-wise
+    # bound grows with the square root of that count (the relative RMS bound does not).
+    nloc = int(np.max(np.sum(ids[sel] < 32, axis=1)))
+    atol = 0.02 * float(np.sqrt(max(1.0, nloc / 2.0)))
+    _compare(got[sel], emu["output"], atol, 0.02, 0.01, f"T={T} {case} vs emulated oracle")
     if case == "few_local":
         assert ws.layout.rows_per_item == 160
         assert np.all(got[640:] == 0)
