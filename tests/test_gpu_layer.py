@@ -7,8 +7,9 @@ Tolerances (bf16 output, compared as float32):
   intermediate (for constructed top-k lists the 0.02 grows as sqrt(max local experts per
   token / 2), since every local expert adds its own flips);
   vs the definition (fp32 intermediate, kernel.py's math without requantisation):
-  |gpu - ref| <= 0.1 + 0.1 |ref| element-wise and relative RMS <= 0.05.
-The fp8 intermediate itself: its scales within 1e-5 relative, and at most 1 code step
+  |gpu - ref| <= 0.25 + 0.1 |ref| element-wise and relative RMS <= 0.05.
+Sizes: T from 1 to 32768 (the largest puts parked GEMM2 rows beyond 2 GiB of the workspace).
+The fp8 intermediate itself: its scales within 3e-4 relative, and at most 1 code step
 apart on at most 1% of the bytes.
 """
 import numpy as np
@@ -19,6 +20,8 @@ from oracle import fp8 as ofp8
 from oracle import layer as olayer
 
 pytestmark = pytest.mark.gpu
+
+TOPK = 8
 
 _WEIGHTS = {}
 
@@ -45,9 +48,12 @@ def _workload(name):
     gh = _gh()
     dev = torch.device("cuda:0")
     w, wnp = _weights()
-    if name == "t256":
-        # a decode batch between the named workloads: 32-row items, separate requantisation
-        logits, bias, hq, hs = gh.inputs.make_activations(256, 1005, dev)
+    if name in ("t256", "t32768"):
+        # t256: a decode batch between the named workloads (32-row items, separate
+        # requantisation); t32768: a long prefill whose parked GEMM2 rows lie beyond 2 GiB of
+        # the workspace (64-bit offsets in GEMM2 and the combine)
+        T, seed = (256, 1005) if name == "t256" else (32768, 1006)
+        logits, bias, hq, hs = gh.inputs.make_activations(T, seed, dev)
         kw = dict(routing_logits=logits, routing_bias=bias, hidden_states=hq, hidden_states_scale=hs,
                   gemm1_weights=w[0], gemm1_weights_scale=w[1], gemm2_weights=w[2], gemm2_weights_scale=w[3],
                   local_expert_offset=0, routed_scaling_factor=gh.inputs.ROUTED_SCALING_FACTOR)
@@ -77,7 +83,7 @@ def _run_full(kw, out_dtype=torch.bfloat16):
 
 
 @pytest.mark.parametrize("name,sample", [("t16", None), ("t64", None), ("t256", None), ("t1024_off64", None),
-                                         ("t8192", 40), ("t4096_skew", 24)])
+                                         ("t8192", 40), ("t4096_skew", 24), ("t32768", 24)])
 def test_layer_matches_oracle(name, sample):
     kw, npkw = _workload(name)
     T = kw["routing_logits"].shape[0]
@@ -107,6 +113,10 @@ def test_layer_matches_oracle(name, sample):
     # tokens with no local expert produce exact zeros
     zero = emu["token_nlocal"] == 0
     assert np.all(got[zero] == 0)
+    if T > 9362:
+        # parked rows (flat slot t*8 + k, 28,672 bytes each) of these tokens start beyond 2 GiB
+        far = tokens[tokens * TOPK * 28672 >= 2 ** 31]
+        assert np.any(emu["token_nlocal"][far] >= 2)
 
 
 @pytest.mark.parametrize("name", ["t64", "t256", "t1024_off64"])
