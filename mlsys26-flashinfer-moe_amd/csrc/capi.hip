@@ -210,8 +210,14 @@ int moe_fp8_run(const moe_fp8_args* args, void* workspace, size_t workspace_byte
   if (args->num_tokens == 0) return MOE_FP8_OK;
   const RouteParams rp = route_params(args, L, workspace, 0);
   const GemmParams gp = gemm_params(args, L, workspace);
-  if (launch_route_dispatch(rp, stream) != hipSuccess) return MOE_FP8_ELAUNCH;
-  if (launch_gemm1(gp, L.rows_per_item, stream) != hipSuccess) return MOE_FP8_ELAUNCH;
+  if (args->num_tokens <= kFusedDispatchTokens) {
+    // routing, then GEMM1 with the dispatch rebuilt in every work-group: one launch less
+    if (launch_route(rp, stream) != hipSuccess) return MOE_FP8_ELAUNCH;
+    if (launch_gemm1_dispatch(gp, rp, stream) != hipSuccess) return MOE_FP8_ELAUNCH;
+  } else {
+    if (launch_route_dispatch(rp, stream) != hipSuccess) return MOE_FP8_ELAUNCH;
+    if (launch_gemm1(gp, L.rows_per_item, stream) != hipSuccess) return MOE_FP8_ELAUNCH;
+  }
   if (launch_requant(gp, L.rows_per_item, stream) != hipSuccess) return MOE_FP8_ELAUNCH;
   if (launch_gemm2(gp, L.rows_per_item, stream) != hipSuccess) return MOE_FP8_ELAUNCH;
   if (launch_combine(gp, stream) != hipSuccess) return MOE_FP8_ELAUNCH;

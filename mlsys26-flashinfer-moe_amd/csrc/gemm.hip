@@ -83,7 +83,8 @@ struct StreamStage {
 // read, and the weight block scales come from lane registers through readlane, so the loop
 // holds no branches and the compiler's waits cover exactly the step being consumed.
 template <int KIND, int NG>
-__device__ __forceinline__ void stream_unit(const GemmParams& p, int e, int r0, int rows, int slice, int lane) {
+__device__ __forceinline__ void stream_unit(const GemmParams& p, int e, int r0, int rows, int slice, int lane,
+                                            const int32_t* row_token) {
   using S = StreamShape<KIND>;
   constexpr int KS = S::kSteps;
   constexpr int NF = S::kFrags;
@@ -127,7 +128,7 @@ __device__ __forceinline__ void stream_unit(const GemmParams& p, int e, int r0, 
     const int m = g * 16 + (lane & 15);
     const int mm = m < rows ? m : 0;
     if constexpr (KIND == kG1) {
-      const int tok = p.sorted_token[r0 + mm];
+      const int tok = row_token[r0 + mm];
       ap[g] = p.hidden + (size_t)tok * kHidden + (lane >> 4) * 16;
       sap[g] = p.hidden_scale + tok;
     } else {
@@ -222,25 +223,153 @@ __device__ __forceinline__ void stream_unit(const GemmParams& p, int e, int r0, 
   }
 }
 
+// The work units of n_items items (item list and GEMM1's bucket-row -> token map in the
+// workspace, or in LDS for the fused dispatch below).
 template <int KIND, int MAXNG>
-__global__ __launch_bounds__(kStreamWaves * 64) void gemm_stream_kernel(GemmParams p) {
+__device__ __forceinline__ void stream_units(const GemmParams& p, int n_items, const int4* items,
+                                             const int32_t* row_token) {
   constexpr int SL = StreamShape<KIND>::kSlices;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int n_items = min(p.counters[kCtrItems], p.max_items);
   const int units = n_items * SL;
   const int nwaves = gridDim.x * kStreamWaves;
   // unit u runs on wavefront (u % gridDim.x, (u / gridDim.x) % kStreamWaves): consecutive
   // units land on different work-groups, i.e. different CUs
   for (int u = wave * gridDim.x + blockIdx.x; u < units; u += nwaves) {
     const int item = u / SL, slice = u - (u / SL) * SL;
-    const int4 it = reinterpret_cast<const int4*>(p.work_items)[item];
+    const int4 it = items[item];
     const int e = __builtin_amdgcn_readfirstlane(it.x);
     const int r0 = __builtin_amdgcn_readfirstlane(it.y);
     const int rows = __builtin_amdgcn_readfirstlane(it.z);
-    if (MAXNG == 1 || rows <= 16) stream_unit<KIND, 1>(p, e, r0, rows, slice, lane);
-    else stream_unit<KIND, MAXNG>(p, e, r0, rows, slice, lane);
+    if (MAXNG == 1 || rows <= 16) stream_unit<KIND, 1>(p, e, r0, rows, slice, lane, row_token);
+    else stream_unit<KIND, MAXNG>(p, e, r0, rows, slice, lane, row_token);
   }
+}
+
+template <int KIND, int MAXNG>
+__global__ __launch_bounds__(kStreamWaves * 64) void gemm_stream_kernel(GemmParams p) {
+  const int n_items = min(p.counters[kCtrItems], p.max_items);
+  stream_units<KIND, MAXNG>(p, n_items, reinterpret_cast<const int4*>(p.work_items), p.sorted_token);
+}
+
+// Decode batches of up to kFusedDispatchTokens tokens: GEMM1 without a dispatch launch before
+// it. Every work-group rebuilds the call's dispatch from the top-k lists in LDS, the same as
+// dispatch_small_kernel produces (kernel.py:252-407 builds the equivalents): per local
+// expert the assignments in ascending flat slot order t*8+k (a stable sort by expert), CSR
+// offsets and the work list of 16-row items. Work-group 0 also writes it to the workspace
+// for the requantisation, GEMM2 and the combine, which run after this kernel. The 512 slots
+// are held two per thread, slot h*256 + tid.
+constexpr int kFusedSlots = kFusedDispatchTokens * kTopK;
+constexpr int kFusedItemRows = 16;
+constexpr int kFusedItems = kExpertsLocal + kFusedSlots / kFusedItemRows;
+constexpr int kFusedHalves = kFusedSlots / (kStreamWaves * 64);
+static_assert(kFusedHalves == 2, "two slots per thread");
+
+struct FusedDispatch {
+  int4 items[kFusedItems];
+  int32_t row_token[kFusedSlots];
+  int cnt[kFusedHalves * kStreamWaves][kExpertsLocal];   // per-wavefront counts -> prefix
+  int start[kExpertsLocal];
+  int n_items;
+};
+
+__device__ __forceinline__ void fused_dispatch(const GemmParams& p, const RouteParams& rp, FusedDispatch& s) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const bool writer = blockIdx.x == 0;
+  const int nslots = p.T * kTopK;
+  const uint64_t lt = lanemask_lt();
+  int le[kFusedHalves], rank[kFusedHalves];
+#pragma unroll
+  for (int h = 0; h < kFusedHalves; ++h) {
+    const int slot = h * kStreamWaves * 64 + tid;
+    const int l = (slot < nslots ? p.topk_ids[slot] : -1) - p.offset;
+    le[h] = slot < nslots && l >= 0 && l < kExpertsLocal ? l : -1;
+  }
+  // stable rank of each slot among the wavefront's slots of its expert, per-wavefront counts
+#pragma unroll
+  for (int h = 0; h < kFusedHalves; ++h) {
+    int c = 0;
+    rank[h] = 0;
+#pragma unroll 4
+    for (int e = 0; e < kExpertsLocal; ++e) {
+      const uint64_t m = __ballot(le[h] == e);
+      if (le[h] == e) rank[h] = __popcll(m & lt);
+      if (lane == e) c = __popcll(m);
+    }
+    if (lane < kExpertsLocal) s.cnt[h * kStreamWaves + wave][lane] = c;
+    if (writer) {
+      // the 8 slots of a token are 8 consecutive lanes
+      const uint64_t m = __ballot(le[h] >= 0);
+      const int slot = h * kStreamWaves * 64 + tid;
+      if ((tid & 7) == 0 && slot < nslots) rp.token_nlocal[slot >> 3] = __popcll((m >> (lane & 56)) & 0xFFull);
+    }
+  }
+  __syncthreads();
+  if (tid < kExpertsLocal) {
+    // lane e of wavefront 0: expert e's wavefront prefix, CSR offset and items
+    const int e = tid;
+    int run = 0;
+#pragma unroll
+    for (int q = 0; q < kFusedHalves * kStreamWaves; ++q) {
+      const int v = s.cnt[q][e];
+      s.cnt[q][e] = run;
+      run += v;
+    }
+    int incl = run;
+#pragma unroll
+    for (int off = 1; off < kExpertsLocal; off <<= 1) {
+      const int o = __shfl_up(incl, off, kExpertsLocal);
+      if (e >= off) incl += o;
+    }
+    const int start = incl - run;
+    s.start[e] = start;
+    const int nch = (run + kFusedItemRows - 1) / kFusedItemRows;
+    int ich = nch;
+#pragma unroll
+    for (int off = 1; off < kExpertsLocal; off <<= 1) {
+      const int o = __shfl_up(ich, off, kExpertsLocal);
+      if (e >= off) ich += o;
+    }
+    const int first = ich - nch;
+    for (int c = 0; c < nch; ++c) {
+      const int4 it = make_int4(e, start + c * kFusedItemRows, min(kFusedItemRows, run - c * kFusedItemRows),
+                                first | (nch << 16));
+      s.items[first + c] = it;
+      if (writer) reinterpret_cast<int4*>(rp.work_items)[first + c] = it;
+    }
+    if (e == kExpertsLocal - 1) s.n_items = ich;
+    if (writer) {
+      rp.expert_count[e] = run;
+      rp.expert_start[e + 1] = incl;
+      if (e == 0) rp.expert_start[0] = 0;
+      if (e == kExpertsLocal - 1) {
+        rp.counters[kCtrAssign] = incl;
+        rp.counters[kCtrItems] = ich;
+      }
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int h = 0; h < kFusedHalves; ++h) {
+    if (le[h] < 0) continue;
+    const int slot = h * kStreamWaves * 64 + tid;
+    const int row = s.start[le[h]] + s.cnt[h * kStreamWaves + wave][le[h]] + rank[h];
+    s.row_token[row] = slot >> 3;
+    if (writer) {
+      rp.sorted_token[row] = slot >> 3;
+      rp.sorted_weight[row] = rp.topk_w[slot];
+      rp.sorted_slot[row] = slot;
+    }
+  }
+  __syncthreads();
+}
+
+__global__ __launch_bounds__(kStreamWaves * 64) void gemm1_stream_dispatch_kernel(GemmParams p, RouteParams rp) {
+  __shared__ FusedDispatch s;
+  fused_dispatch(p, rp, s);
+  stream_units<kG1, 1>(p, s.n_items, s.items, s.row_token);
 }
 
 // Requantises the fp32 SwiGLU rows: per row and 128 columns, scale = max(amax/448, 1e-12)
@@ -388,6 +517,16 @@ hipError_t launch_stream(const GemmParams& p, int rows_per_item, hipStream_t s) 
 hipError_t launch_gemm1(const GemmParams& p, int rows_per_item, hipStream_t s) {
   if (rows_per_item > 32) return launch_gemm1_tile(p, rows_per_item, s);
   return launch_stream<kG1>(p, rows_per_item, s);
+}
+
+hipError_t launch_gemm1_dispatch(const GemmParams& p, const RouteParams& rp, hipStream_t s) {
+  static int occ = 0;
+  if (p.T <= 0 || p.T > kFusedDispatchTokens || rp.rows_per_item != kFusedItemRows) return hipErrorInvalidValue;
+  int grid = num_cus() * resident_per_cu(gemm1_stream_dispatch_kernel, occ);
+  const int cap = (kFusedItems * StreamShape<kG1>::kSlices + kStreamWaves - 1) / kStreamWaves;
+  if (grid > cap) grid = cap;
+  hipLaunchKernelGGL(gemm1_stream_dispatch_kernel, dim3(grid), dim3(kStreamWaves * 64), 0, s, p, rp);
+  return hipGetLastError();
 }
 
 hipError_t launch_requant(const GemmParams& p, int rows_per_item, hipStream_t s) {

@@ -4,6 +4,8 @@
 //   caller tensors   : the contract of kernel.py:591-607 (see include/moe_fp8.h)
 //   workspace arrays : moe_fp8_layout offsets; every array is 256-byte aligned.
 // Kernels of one call run in this order on one stream:
+//   T <= 64 (moe_fp8_run): route_kernel<false> -> gemm1_stream_dispatch_kernel (GEMM1 that
+//   rebuilds the dispatch itself) -> requant_kernel -> GEMM2 -> combine_kernel; otherwise
 //   route_dispatch_small_kernel | (route_kernel<false> -> dispatch_small_kernel)
 //   | (route_kernel<true> -> scan_kernel -> place_kernel)
 //   -> GEMM1 -> [requant_kernel] -> GEMM2 -> combine_kernel
@@ -37,6 +39,9 @@ constexpr int kRouteTokensPerBlock = 16;
 constexpr int kRouteThreads = 1024;
 // Up to this many tokens routing and dispatch run in a single work-group (one launch).
 constexpr int kSinglePassTokens = 256;
+// Up to this many tokens moe_fp8_run launches routing alone, and every GEMM1 work-group
+// rebuilds the dispatch in LDS (work-group 0 also writes it to the workspace).
+constexpr int kFusedDispatchTokens = 64;
 
 // Control block (workspace counters[]).
 constexpr int kCtrItems = 0;    // number of GEMM work items
@@ -119,7 +124,9 @@ struct GemmParams {
 };
 
 hipError_t launch_route_dispatch(const RouteParams& p, hipStream_t s);
+hipError_t launch_route(const RouteParams& p, hipStream_t s);
 hipError_t launch_gemm1(const GemmParams& p, int rows_per_item, hipStream_t s);
+hipError_t launch_gemm1_dispatch(const GemmParams& p, const RouteParams& rp, hipStream_t s);
 hipError_t launch_requant(const GemmParams& p, int rows_per_item, hipStream_t s);
 hipError_t launch_gemm2(const GemmParams& p, int rows_per_item, hipStream_t s);
 hipError_t launch_combine(const GemmParams& p, hipStream_t s);

@@ -516,6 +516,11 @@ __global__ __launch_bounds__(kRouteTokensPerBlock * kTopK) void place_kernel(Rou
   p.sorted_slot[pos] = s;
 }
 
+hipError_t launch_route(const RouteParams& p, hipStream_t s) {
+  hipLaunchKernelGGL(route_kernel<false>, dim3(p.nblocks), dim3(kRouteWaves * 64), 0, s, p);
+  return hipGetLastError();
+}
+
 hipError_t launch_route_dispatch(const RouteParams& p, hipStream_t s) {
   if (p.single_pass && !p.skip_routing && p.T <= kFusedRouteTokens) {
     hipLaunchKernelGGL(route_dispatch_small_kernel, dim3(1), dim3(kRouteThreads), 0, s, p);

@@ -7,6 +7,7 @@ import numpy as np
 import torch
 
 import __graft_entry__ as ge
+from oracle import dispatch as odsp
 
 pkg = ge.load_package()
 from mlsys26_flashinfer_moe_amd import _lib, inputs  # noqa: E402
@@ -95,3 +96,29 @@ def to_numpy_inputs(kw: dict) -> dict:
         local_expert_offset=kw["local_expert_offset"],
         routed_scaling_factor=kw["routed_scaling_factor"],
     )
+
+
+def check_dispatch(ws: Workspace, ids: np.ndarray, w: np.ndarray, offset: int, T: int):
+    """The workspace's dispatch arrays are bit-exact with the oracle's dispatch of (ids, w)."""
+    d = odsp.dispatch(ids, w, offset)
+    n = int(d["expert_start"][-1])
+    c = counters(ws)
+    assert c[1] == n
+    assert np.array_equal(read(ws, "expert_count", torch.int32, 32), d["expert_count"])
+    assert np.array_equal(read(ws, "expert_start", torch.int32, 33), d["expert_start"])
+    assert np.array_equal(read(ws, "sorted_slot", torch.int32, n), d["sorted_slot"])
+    assert np.array_equal(read(ws, "sorted_token", torch.int32, n), d["sorted_token"])
+    assert np.array_equal(read(ws, "sorted_weight", torch.float32, n).view(np.uint32),
+                          d["sorted_weight"].view(np.uint32))
+    assert np.array_equal(read(ws, "token_nlocal", torch.int32, T), d["token_nlocal"])
+    rpi = int(ws.layout.rows_per_item)
+    items = odsp.work_items(d["expert_count"], d["expert_start"], rpi)
+    assert c[0] == len(items)
+    got = read(ws, "work_items", torch.int32, 4 * len(items)).reshape(-1, 4)
+    assert np.array_equal(got, items)
+    # every bucket row is covered exactly once by the work list
+    cover = np.zeros(n, dtype=np.int32)
+    for e, r0, rows, _ in items:
+        assert d["expert_start"][e] <= r0 and r0 + rows <= d["expert_start"][e + 1] and 0 < rows <= rpi
+        cover[r0:r0 + rows] += 1
+    assert np.all(cover == 1)

@@ -18,6 +18,7 @@ import torch
 
 from oracle import fp8 as ofp8
 from oracle import layer as olayer
+from oracle import routing as orouting
 
 pytestmark = pytest.mark.gpu
 
@@ -117,6 +118,40 @@ def test_layer_matches_oracle(name, sample):
         # parked rows (flat slot t*8 + k, 28,672 bytes each) of these tokens start beyond 2 GiB
         far = tokens[tokens * TOPK * 28672 >= 2 ** 31]
         assert np.any(emu["token_nlocal"][far] >= 2)
+
+
+@pytest.mark.parametrize("T,offset", [(1, 0), (16, 0), (40, 224), (64, 0), (64, 96)])
+def test_run_rebuilds_dispatch_in_gemm1(T, offset):
+    """Up to 64 tokens moe_fp8_run launches routing alone, and every GEMM1 work-group rebuilds
+    the dispatch in LDS; work-group 0 writes it to the workspace for the later kernels. That
+    dispatch is bit-exact with the oracle's, and the output is bit-equal to the stage entry
+    points' (routing and dispatch launched before GEMM1)."""
+    gh = _gh()
+    dev = torch.device("cuda:0")
+    w, _ = _weights()
+    print(f"run with dispatch in GEMM1: T={T} offset={offset}", flush=True)
+    logits, bias, hq, hs = gh.inputs.make_activations(T, 3000 + T + offset, dev)
+    rsf = gh.inputs.ROUTED_SCALING_FACTOR
+    kw = dict(routing_logits=logits, routing_bias=bias, hidden_states=hq, hidden_states_scale=hs,
+              gemm1_weights=w[0], gemm1_weights_scale=w[1], gemm2_weights=w[2], gemm2_weights_scale=w[3],
+              local_expert_offset=offset, routed_scaling_factor=rsf)
+    out = torch.full((T, 7168), float("nan"), dtype=torch.bfloat16, device=dev)
+    ws = gh.new_workspace(T, dev)
+    gh.run_layer(gh.make_args(**kw, output=out), ws)
+    ids = gh.read(ws, "topk_ids", torch.int32, T * 8).reshape(T, 8)
+    wts = gh.read(ws, "topk_weights", torch.float32, T * 8).reshape(T, 8)
+    rid, rw = orouting.route(logits.cpu().numpy(), bias.float().cpu().numpy(), rsf)
+    assert np.array_equal(ids, rid)
+    assert np.array_equal(wts.view(np.uint32), rw.view(np.uint32))
+    gh.check_dispatch(ws, rid, rw, offset, T)
+    staged = torch.full((T, 7168), float("nan"), dtype=torch.bfloat16, device=dev)
+    ws2 = gh.new_workspace(T, dev)
+    args2 = gh.make_args(**kw, output=staged)
+    gh.route_dispatch(args2, ws2)
+    gh.gemm1(args2, ws2)
+    gh.gemm2_combine(args2, ws2)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), staged.view(torch.int16))
 
 
 @pytest.mark.parametrize("name", ["t64", "t256", "t1024_off64"])

@@ -8,7 +8,6 @@ import numpy as np
 import pytest
 import torch
 
-from oracle import dispatch as odsp
 from oracle import routing as orouting
 
 pytestmark = pytest.mark.gpu
@@ -36,31 +35,6 @@ def _route_gpu(logits_np, bias_np, offset=0, rsf=2.5, bias_dtype=torch.float32):
     return ws, gh
 
 
-def _check_dispatch(ws, gh, ids, w, offset, T):
-    d = odsp.dispatch(ids, w, offset)
-    n = int(d["expert_start"][-1])
-    c = gh.counters(ws)
-    assert c[1] == n
-    assert np.array_equal(gh.read(ws, "expert_count", torch.int32, 32), d["expert_count"])
-    assert np.array_equal(gh.read(ws, "expert_start", torch.int32, 33), d["expert_start"])
-    assert np.array_equal(gh.read(ws, "sorted_slot", torch.int32, n), d["sorted_slot"])
-    assert np.array_equal(gh.read(ws, "sorted_token", torch.int32, n), d["sorted_token"])
-    assert np.array_equal(gh.read(ws, "sorted_weight", torch.float32, n).view(np.uint32),
-                          d["sorted_weight"].view(np.uint32))
-    assert np.array_equal(gh.read(ws, "token_nlocal", torch.int32, T), d["token_nlocal"])
-    rpi = int(ws.layout.rows_per_item)
-    items = odsp.work_items(d["expert_count"], d["expert_start"], rpi)
-    assert c[0] == len(items)
-    got = gh.read(ws, "work_items", torch.int32, 4 * len(items)).reshape(-1, 4)
-    assert np.array_equal(got, items)
-    # every bucket row is covered exactly once by the work list
-    cover = np.zeros(n, dtype=np.int32)
-    for e, r0, rows, _ in items:
-        assert d["expert_start"][e] <= r0 and r0 + rows <= d["expert_start"][e + 1] and 0 < rows <= rpi
-        cover[r0:r0 + rows] += 1
-    assert np.all(cover == 1)
-
-
 @pytest.mark.parametrize("part", [0, 1, 2])
 def test_routing_bit_exact_on_golden_logits(part):
     m = GOLD["bias_index"] == part
@@ -74,7 +48,7 @@ def test_routing_bit_exact_on_golden_logits(part):
     assert np.array_equal(w.view(np.uint32), rw.view(np.uint32))
     # and the independent router's expert sets
     assert np.array_equal(np.sort(ids, axis=1), GOLD["ids_sorted"][m])
-    _check_dispatch(ws, gh, rid, rw, 0, T)
+    gh.check_dispatch(ws, rid, rw, 0, T)
 
 
 @pytest.mark.parametrize("bias_dtype", [torch.float32, torch.bfloat16, torch.float16])
@@ -117,7 +91,7 @@ def test_dispatch_matches_oracle(T, offset):
     ws, gh = _route_gpu(logits, bias, offset=offset)
     rid, rw = orouting.route(logits, bias, 2.5)
     assert np.array_equal(gh.read(ws, "topk_ids", torch.int32, T * 8).reshape(T, 8), rid)
-    _check_dispatch(ws, gh, rid, rw, offset, T)
+    gh.check_dispatch(ws, rid, rw, offset, T)
 
 
 @pytest.mark.parametrize("T", [60, 300])
@@ -145,7 +119,7 @@ def test_dispatch_given_topk(case, T):
     args = gh.routing_args(logits, torch.zeros(256, device=dev), 0, 1.0)
     print(f"dispatch given top-k case={case}", flush=True)
     gh.route_dispatch(args, ws, skip_routing=1)
-    _check_dispatch(ws, gh, ids, w, 0, T)
+    gh.check_dispatch(ws, ids, w, 0, T)
     # the given lists are left untouched
     assert np.array_equal(gh.read(ws, "topk_ids", torch.int32, T * 8).reshape(T, 8), ids)
 
@@ -165,4 +139,4 @@ def test_workspace_reuse_across_calls():
         args = gh.routing_args(lt, bt, off, 2.5)
         gh.route_dispatch(args, ws)
         rid, rw = orouting.route(logits, bias, 2.5)
-        _check_dispatch(ws, gh, rid, rw, off, T)
+        gh.check_dispatch(ws, rid, rw, off, T)
