@@ -287,18 +287,21 @@ __device__ __forceinline__ void fused_dispatch(const GemmParams& p, const RouteP
     const int l = (slot < nslots ? p.topk_ids[slot] : -1) - p.offset;
     le[h] = slot < nslots && l >= 0 && l < kExpertsLocal ? l : -1;
   }
-  // stable rank of each slot among the wavefront's slots of its expert, per-wavefront counts
+  // stable rank of each slot among the wavefront's slots of its expert, per-wavefront counts:
+  // one ballot per distinct local expert of the wavefront (a few at decode sizes)
 #pragma unroll
   for (int h = 0; h < kFusedHalves; ++h) {
-    int c = 0;
+    int* cnt = s.cnt[h * kStreamWaves + wave];
+    if (lane < kExpertsLocal) cnt[lane] = 0;
     rank[h] = 0;
-#pragma unroll 4
-    for (int e = 0; e < kExpertsLocal; ++e) {
-      const uint64_t m = __ballot(le[h] == e);
-      if (le[h] == e) rank[h] = __popcll(m & lt);
-      if (lane == e) c = __popcll(m);
+    uint64_t todo = __ballot(le[h] >= 0);
+    while (todo) {
+      const int v = __builtin_amdgcn_readlane(le[h], __builtin_ctzll(todo));
+      const uint64_t m = __ballot(le[h] == v);
+      if (le[h] == v) rank[h] = __popcll(m & lt);
+      if (lane == 0) cnt[v] = __popcll(m);
+      todo &= ~m;
     }
-    if (lane < kExpertsLocal) s.cnt[h * kStreamWaves + wave][lane] = c;
     if (writer) {
       // the 8 slots of a token are 8 consecutive lanes
       const uint64_t m = __ballot(le[h] >= 0);
