@@ -156,7 +156,9 @@ int moe_fp8_workspace_layout(int32_t num_tokens, moe_fp8_layout* layout);
 int moe_fp8_workspace_init(void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 /* The whole layer: routing, dispatch, GEMM1+SwiGLU+requant, GEMM2+weighted combine.
- * Replaces run() (kernel.py:562-729). */
+ * Up to 64 tokens the dispatch is rebuilt inside the GEMM1 kernel instead of launched
+ * before it; afterwards the workspace holds the same dispatch arrays as after the stage
+ * entry points. Replaces run() (kernel.py:562-729). */
 int moe_fp8_run(const moe_fp8_args* args, void* workspace, size_t workspace_bytes,
                 hipStream_t stream);
 
