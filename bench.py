@@ -14,20 +14,24 @@ Three independent weight sets are rotated across steps so that every step stream
 weights from HBM (1.41 GB per set, far above the 256 MB last-level cache).
 
 The JSON line also carries:
-  roofline      the dominant kernel (GEMM1 at T<=1024, else the larger GEMM) timed with HIP
-                events on the launch stream inside the timed region of a staged run;
+  roofline      the dominant kernel, GEMM1 (the one kernel of stage 2 of moe_fp8_run: up to 64
+                tokens gemm1_stream_dispatch_kernel), timed with HIP events that the library
+                records on the launch stream between the stages (moe_fp8_run_profiled);
   cpu_baseline  the numpy oracle (fp32 dequantise-and-matmul) on the same workload, timed on
                 the host cores (median of 5 runs; the host's CPU model and count beside it);
   workloads     the same figures for the other four workloads (T=16, 1024 with offset 64,
                 8192, 4096 skewed), each with the upstream activation quantiser
                 (quantize_hidden: bf16 [T,7168] -> e4m3fn + scales [56,T]) timed beside the
                 layer; its bytes are T * 21,728 (14,336 read, 7,168 + 224 written).
-Per workload, us_per_step is the mean over the K timed calls (one event pair around all K);
-us_median_call is the median of K calls timed one by one in a separate pass.
+Per workload, us_per_step is the mean over the K timed C-ABI calls (one event pair around all
+K); run_py_us_per_step the same through the Python entry point run() (argument checks,
+workspace lookup and ctypes packing included; run_py_wall_us_per_step is its host wall
+clock); us_median_call is the median of K calls timed one by one in a separate pass.
 """
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -73,13 +77,29 @@ def routing_stats(ws, T):
     return n, e_touched, u
 
 
-def workload_figures(T, n, e_touched, u):
+def workload_figures(T, n, e_touched, u, rows_per_item):
+    """Algorithmic work of the layer and of its GEMM1 kernel. GEMM1 reads the touched experts'
+    W13 and block scales and each token's hidden row and scales once; in the decode regime
+    (items of <= 32 rows) it writes each assignment's fp32 SwiGLU row (8,192 B) and reads the
+    top-k lists (64 B per token, for the dispatch it rebuilds up to 64 tokens); on the tile path
+    it writes the requantised fp8 row and its 16 scales (2,112 B)."""
     layer_bytes = e_touched * BYTES_PER_EXPERT + T * BYTES_PER_TOKEN + 512
     layer_flops = n * FLOPS_PER_ASSIGNMENT
-    g1_bytes = e_touched * G1_BYTES_PER_EXPERT + u * (7168 + 224) + n * (2048 + 64)
-    g2_bytes = e_touched * G2_BYTES_PER_EXPERT + n * (2048 + 64) + T * 14_336
-    return dict(layer_bytes=layer_bytes, layer_flops=layer_flops, g1_bytes=g1_bytes, g2_bytes=g2_bytes,
+    if rows_per_item <= 32:
+        g1_bytes = e_touched * G1_BYTES_PER_EXPERT + u * (7168 + 224) + n * 2048 * 4 + T * 64
+    else:
+        g1_bytes = e_touched * G1_BYTES_PER_EXPERT + u * (7168 + 224) + n * (2048 + 64)
+    return dict(layer_bytes=layer_bytes, layer_flops=layer_flops, g1_bytes=g1_bytes,
                 g1_flops=n * G1_FLOPS_PER_ASSIGNMENT, g2_flops=n * G2_FLOPS_PER_ASSIGNMENT)
+
+
+def gemm1_kernel_name(T, rows_per_item):
+    """The one kernel of stage 2 (GEMM1) in moe_fp8_run for a batch of T tokens."""
+    if T <= 64:
+        return "gemm1_stream_dispatch_kernel", "gemm1_stream_dispatch"
+    if rows_per_item <= 32:
+        return "gemm_stream_kernel<1, 2>", "gemm1_stream"
+    return f"gemm_tile_kernel<true, {160 if rows_per_item > 128 else 128}>", "gemm1_tile"
 
 
 def bench_workload(pkg, inputs, name, weight_sets, steps, warmup):
@@ -115,7 +135,7 @@ def bench_workload(pkg, inputs, name, weight_sets, steps, warmup):
     torch.cuda.synchronize()
     n, e_touched, u = routing_stats(ws, T)
 
-    # whole-layer timing: K steps between two synchronisations
+    # whole-layer timing through the C ABI: K steps between two synchronisations
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -127,6 +147,25 @@ def bench_workload(pkg, inputs, name, weight_sets, steps, warmup):
     wall = time.perf_counter() - t0
     ms_per_step = ev0.elapsed_time(ev1) / steps
 
+    # the same K steps through the Python entry point run() (validation, workspace lookup and
+    # argument packing included), host wall clock and HIP events
+    kwsets = []
+    for w in weight_sets:
+        k2 = dict(kw)
+        k2.update(gemm1_weights=w[0], gemm1_weights_scale=w[1], gemm2_weights=w[2], gemm2_weights_scale=w[3])
+        kwsets.append(k2)
+    for i in range(min(warmup, 3)):
+        pkg.run(**kwsets[i % R], output=out)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    ev0.record(stream)
+    for i in range(steps):
+        pkg.run(**kwsets[i % R], output=out)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    run_wall = time.perf_counter() - t1
+    run_ms = ev0.elapsed_time(ev1) / steps
+
     # per-call timing: an event before every call, for the median call duration
     pev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
     for i in range(steps):
@@ -137,18 +176,17 @@ def bench_workload(pkg, inputs, name, weight_sets, steps, warmup):
     call_ms = sorted(pev[i].elapsed_time(pev[i + 1]) for i in range(steps))
     median_ms = call_ms[steps // 2] if steps % 2 else 0.5 * (call_ms[steps // 2 - 1] + call_ms[steps // 2])
 
-    # staged timing with HIP events around each stage on the launch stream
+    # stage timing of the same launches (moe_fp8_run_profiled): HIP events recorded by the
+    # library on the launch stream between routing [+ dispatch], GEMM1 (one kernel) and
+    # requantisation + GEMM2 + combine
     evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(steps)]
+    for e in evs:
+        for x in e:
+            x.record(stream)   # creates the underlying HIP event
+    torch.cuda.synchronize()
     for i in range(steps):
-        a = argsets[i % R]
-        e = evs[i]
-        e[0].record(stream)
-        _lib.check(lib.moe_fp8_route_dispatch(a, 0, ws.ptr, nbytes, sptr), "route_dispatch")
-        e[1].record(stream)
-        _lib.check(lib.moe_fp8_gemm1(a, ws.ptr, nbytes, sptr), "gemm1")
-        e[2].record(stream)
-        _lib.check(lib.moe_fp8_gemm2_combine(a, ws.ptr, nbytes, sptr), "gemm2_combine")
-        e[3].record(stream)
+        hev = (ctypes.c_void_p * 4)(*[x.cuda_event for x in evs[i]])
+        _lib.check(lib.moe_fp8_run_profiled(argsets[i % R], ws.ptr, nbytes, sptr, hev), "moe_fp8_run_profiled")
     torch.cuda.synchronize()
     stage_ms = [sum(evs[i][j].elapsed_time(evs[i][j + 1]) for i in range(steps)) / steps for j in range(3)]
 
@@ -174,16 +212,18 @@ def bench_workload(pkg, inputs, name, weight_sets, steps, warmup):
     q_bytes = T * (7168 * 2 + 7168 + 56 * 4)
     del qsets
 
-    f = workload_figures(T, n, e_touched, u)
+    rpi = int(ws.layout.rows_per_item)
+    f = workload_figures(T, n, e_touched, u, rpi)
     us = ms_per_step * 1e3
     res = dict(T=T, offset=wl.local_expert_offset, assignments=n, experts_touched=e_touched,
                us_per_step=round(us, 2), us_median_call=round(median_ms * 1e3, 2),
                wall_us_per_step=round(wall / steps * 1e6, 2),
+               run_py_us_per_step=round(run_ms * 1e3, 2), run_py_wall_us_per_step=round(run_wall / steps * 1e6, 2),
                hbm_gbs=round(f["layer_bytes"] / (us * 1e-6) / 1e9, 1),
                tflops=round(f["layer_flops"] / (us * 1e-6) / 1e12, 2),
                stage_us=dict(route_dispatch=round(stage_ms[0] * 1e3, 2), gemm1=round(stage_ms[1] * 1e3, 2),
-                             gemm2_combine=round(stage_ms[2] * 1e3, 2)))
-    res["rows_per_item"] = int(ws.layout.rows_per_item)
+                             requant_gemm2_combine=round(stage_ms[2] * 1e3, 2)))
+    res["rows_per_item"] = rpi
     res["hbm_roofline_frac"] = round(res["hbm_gbs"] / HBM_PEAK_GBS, 4)
     res["mfma_roofline_frac"] = round(res["tflops"] / FP8_PEAK_TFLOPS, 4)
     q_gbs = q_bytes / (q_us * 1e-6) / 1e9
@@ -285,15 +325,12 @@ def main():
 
     m = results[args.workload]
     T = m["T"]
-    # Dominant kernel: GEMM1, the one kernel of stage 2 (W13 is two thirds of the weight
-    # bytes); HBM-bound up to T = 1024, MFMA-bound above. Its launch duration is the HIP-event
-    # time of stage 2 on the launch stream.
+    # Dominant kernel: GEMM1, the one kernel of stage 2 of moe_fp8_run (W13 is two thirds of the
+    # weight bytes); HBM-bound up to T = 1024, MFMA-bound above. Its launch duration is the
+    # HIP-event time of stage 2, recorded by the library on the launch stream.
     g1_ms = main_stage[1]
     rpi = m["rows_per_item"]
-    if rpi <= 32:
-        kernel, tag = f"gemm_stream_kernel<1, {1 if rpi <= 16 else 2}>", "gemm1_stream"
-    else:
-        kernel, tag = f"gemm_tile_kernel<true, {160 if rpi > 128 else 128}>", "gemm1_tile"
+    kernel, tag = gemm1_kernel_name(T, rpi)
     if T <= 1024:
         roof = dict(kernel=kernel, bound="hbm", achieved=round(main_f["g1_bytes"] / (g1_ms * 1e-3) / 1e9, 1),
                     peak=HBM_PEAK_GBS, unit="GB/s")

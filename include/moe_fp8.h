@@ -110,6 +110,11 @@ typedef struct moe_fp8_args {
  *                                   (the tile kernels' work-list state)
  *   act           fp8   [N_max, 2048]    SwiGLU output requantised to e4m3fn          (kernel.py:669)
  *   act_scale     fp32  [N_max, 16]      its 1x128 block scales, row-major per row   (kernel.py:670)
+ *                 Deliberate difference: the reference requantises per 1x64 block (BLOCK_N_1 = 64,
+ *                 kernel.py:131-135, :643, scales [32, N]); this layer per 1x128, so that GEMM2
+ *                 applies one activation scale per 128-wide K block, like every other operand.
+ *                 The parity tests bound the output's distance from fp32 math by that of the
+ *                 64-column algorithm (per token at most 2x its maximum error + 1/64).
  *   partial       fp32  [T*8, 7168]      weighted GEMM2 rows of tokens with more than one local
  *                                        assignment, indexed by flat slot             (kernel.py:704)
  *   swiglu        fp32  [N_max, 2048]    SwiGLU output before requantisation; only for
@@ -147,10 +152,11 @@ size_t moe_fp8_workspace_bytes(int32_t num_tokens);
 /* Fills *layout for num_tokens tokens. Returns MOE_FP8_OK or MOE_FP8_EINVAL_*. */
 int moe_fp8_workspace_layout(int32_t num_tokens, moe_fp8_layout* layout);
 
-/* Clears the workspace's control block. A freshly allocated workspace must be passed
- * through this once before its first use (so that a GEMM stage run before any dispatch
- * finds no work); every dispatch rewrites the control block before the GEMMs read it,
- * so one workspace is reusable by successive calls on one stream without clearing.
+/* Clears the workspace's control block with a one-work-group kernel (never a memset, so a
+ * call captured into a HIP graph records a kernel node). A freshly allocated workspace must
+ * be passed through this once before its first use (so that a GEMM stage run before any
+ * dispatch finds no work); every dispatch rewrites the control block before the GEMMs read
+ * it, so one workspace is reusable by successive calls on one stream without clearing.
  * Calls that overlap in time must use different workspaces. No counterpart in the
  * reference, whose temporaries are freshly zeroed torch tensors (kernel.py:348, 669-670, 704). */
 int moe_fp8_workspace_init(void* workspace, size_t workspace_bytes, hipStream_t stream);
@@ -161,6 +167,16 @@ int moe_fp8_workspace_init(void* workspace, size_t workspace_bytes, hipStream_t 
  * entry points. Replaces run() (kernel.py:562-729). */
 int moe_fp8_run(const moe_fp8_args* args, void* workspace, size_t workspace_bytes,
                 hipStream_t stream);
+
+/* moe_fp8_run with stage timing: the same launches, with events[0] recorded on `stream` before
+ * stage 1 (routing, and the dispatch above 64 tokens), events[1] before stage 2 (GEMM1, one
+ * kernel; up to 64 tokens it also rebuilds the dispatch), events[2] before stage 3
+ * (requantisation, GEMM2 and the combine) and events[3] after it. The events must have been
+ * created by the caller (hipEventCreate) on the stream's device. Replaces run() (kernel.py:562-729)
+ * like moe_fp8_run; the per-stage split mirrors its routing (:624-639), dispatch + GEMM1
+ * (:649-693) and GEMM2 + finalize (:695-729) sections. */
+int moe_fp8_run_profiled(const moe_fp8_args* args, void* workspace, size_t workspace_bytes,
+                         hipStream_t stream, hipEvent_t events[4]);
 
 /* Stage 1: routing and dispatch. Writes topk_ids/topk_weights, the expert histogram,
  * CSR offsets, sorted permutation and the GEMM work list. With skip_routing != 0 the

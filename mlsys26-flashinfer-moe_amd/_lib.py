@@ -45,6 +45,7 @@ EXPORTED_SYMBOLS = (
     "moe_fp8_workspace_layout",
     "moe_fp8_workspace_init",
     "moe_fp8_run",
+    "moe_fp8_run_profiled",
     "moe_fp8_route_dispatch",
     "moe_fp8_gemm1",
     "moe_fp8_gemm2_combine",
@@ -131,6 +132,8 @@ def load() -> ctypes.CDLL:
         lib.moe_fp8_workspace_init.restype = ctypes.c_int
         lib.moe_fp8_run.argtypes = [args_p, vp, sz, vp]
         lib.moe_fp8_run.restype = ctypes.c_int
+        lib.moe_fp8_run_profiled.argtypes = [args_p, vp, sz, vp, ctypes.POINTER(vp)]
+        lib.moe_fp8_run_profiled.restype = ctypes.c_int
         lib.moe_fp8_route_dispatch.argtypes = [args_p, i32, vp, sz, vp]
         lib.moe_fp8_route_dispatch.restype = ctypes.c_int
         lib.moe_fp8_gemm1.argtypes = [args_p, vp, sz, vp]

@@ -103,7 +103,18 @@ GemmParams gemm_params(const moe_fp8_args* a, const moe_fp8_layout& L, void* ws)
   return p;
 }
 
+// Zeroes the control block with ordinary vector stores: a kernel node, never a memset node,
+// when a caller captures the call into a graph.
+__global__ __launch_bounds__(64) void clear_control_kernel(int32_t* counters) {
+  for (int i = threadIdx.x; i < kNumCounters; i += 64) counters[i] = 0;
+}
+
 }  // namespace
+
+hipError_t launch_clear_control(int32_t* counters, hipStream_t s) {
+  hipLaunchKernelGGL(clear_control_kernel, dim3(1), dim3(64), 0, s, counters);
+  return hipGetLastError();
+}
 
 int compute_layout(int32_t T, moe_fp8_layout* out) {
   if (!out) return MOE_FP8_EINVAL_POINTER;
@@ -147,6 +158,36 @@ int compute_layout(int32_t T, moe_fp8_layout* out) {
   return MOE_FP8_OK;
 }
 
+namespace {
+
+// The launch sequence of moe_fp8_run; with `events`, events[i] is recorded on the stream
+// before stage i+1 (routing [+ dispatch], GEMM1, requantisation + GEMM2 + combine) and
+// events[3] after the last launch.
+int run_layer(const moe_fp8_args* args, void* workspace, size_t workspace_bytes, hipStream_t stream,
+              hipEvent_t* events) {
+  moe_fp8_layout L;
+  const int rc = check_args(args, true, workspace, workspace_bytes, &L);
+  if (rc != MOE_FP8_OK) return rc;
+  if (args->num_tokens == 0) return MOE_FP8_OK;
+  const RouteParams rp = route_params(args, L, workspace, 0);
+  const GemmParams gp = gemm_params(args, L, workspace);
+  auto mark = [&](int i) { return !events || hipEventRecord(events[i], stream) == hipSuccess; };
+  if (!mark(0)) return MOE_FP8_ELAUNCH;
+  if (args->num_tokens <= kFusedDispatchTokens) {
+    // routing, then GEMM1 with the dispatch rebuilt in every work-group: one launch less
+    if (launch_route(rp, stream) != hipSuccess || !mark(1)) return MOE_FP8_ELAUNCH;
+    if (launch_gemm1_dispatch(gp, rp, stream) != hipSuccess || !mark(2)) return MOE_FP8_ELAUNCH;
+  } else {
+    if (launch_route_dispatch(rp, stream) != hipSuccess || !mark(1)) return MOE_FP8_ELAUNCH;
+    if (launch_gemm1(gp, L.rows_per_item, stream) != hipSuccess || !mark(2)) return MOE_FP8_ELAUNCH;
+  }
+  if (launch_requant(gp, L.rows_per_item, stream) != hipSuccess) return MOE_FP8_ELAUNCH;
+  if (launch_gemm2(gp, L.rows_per_item, stream) != hipSuccess) return MOE_FP8_ELAUNCH;
+  if (launch_combine(gp, stream) != hipSuccess || !mark(3)) return MOE_FP8_ELAUNCH;
+  return MOE_FP8_OK;
+}
+
+}  // namespace
 }  // namespace moe
 
 using namespace moe;
@@ -165,9 +206,8 @@ int moe_fp8_workspace_layout(int32_t num_tokens, moe_fp8_layout* layout) {
 
 int moe_fp8_workspace_init(void* workspace, size_t workspace_bytes, hipStream_t stream) {
   if (!workspace || workspace_bytes < kNumCounters * sizeof(int32_t)) return MOE_FP8_EWORKSPACE;
-  if (hipMemsetAsync(workspace, 0, kNumCounters * sizeof(int32_t), stream) != hipSuccess)
-    return MOE_FP8_ELAUNCH;
-  return MOE_FP8_OK;
+  return launch_clear_control(static_cast<int32_t*>(workspace), stream) == hipSuccess ? MOE_FP8_OK
+                                                                                      : MOE_FP8_ELAUNCH;
 }
 
 int moe_fp8_route_dispatch(const moe_fp8_args* args, int32_t skip_routing, void* workspace,
@@ -202,26 +242,16 @@ int moe_fp8_gemm2_combine(const moe_fp8_args* args, void* workspace, size_t work
   return launch_combine(p, stream) == hipSuccess ? MOE_FP8_OK : MOE_FP8_ELAUNCH;
 }
 
+
 int moe_fp8_run(const moe_fp8_args* args, void* workspace, size_t workspace_bytes,
                 hipStream_t stream) {
-  moe_fp8_layout L;
-  const int rc = check_args(args, true, workspace, workspace_bytes, &L);
-  if (rc != MOE_FP8_OK) return rc;
-  if (args->num_tokens == 0) return MOE_FP8_OK;
-  const RouteParams rp = route_params(args, L, workspace, 0);
-  const GemmParams gp = gemm_params(args, L, workspace);
-  if (args->num_tokens <= kFusedDispatchTokens) {
-    // routing, then GEMM1 with the dispatch rebuilt in every work-group: one launch less
-    if (launch_route(rp, stream) != hipSuccess) return MOE_FP8_ELAUNCH;
-    if (launch_gemm1_dispatch(gp, rp, stream) != hipSuccess) return MOE_FP8_ELAUNCH;
-  } else {
-    if (launch_route_dispatch(rp, stream) != hipSuccess) return MOE_FP8_ELAUNCH;
-    if (launch_gemm1(gp, L.rows_per_item, stream) != hipSuccess) return MOE_FP8_ELAUNCH;
-  }
-  if (launch_requant(gp, L.rows_per_item, stream) != hipSuccess) return MOE_FP8_ELAUNCH;
-  if (launch_gemm2(gp, L.rows_per_item, stream) != hipSuccess) return MOE_FP8_ELAUNCH;
-  if (launch_combine(gp, stream) != hipSuccess) return MOE_FP8_ELAUNCH;
-  return MOE_FP8_OK;
+  return run_layer(args, workspace, workspace_bytes, stream, nullptr);
+}
+
+int moe_fp8_run_profiled(const moe_fp8_args* args, void* workspace, size_t workspace_bytes,
+                         hipStream_t stream, hipEvent_t events[4]) {
+  if (!events || !events[0] || !events[1] || !events[2] || !events[3]) return MOE_FP8_EINVAL_POINTER;
+  return run_layer(args, workspace, workspace_bytes, stream, events);
 }
 
 int moe_fp8_quantize_hidden(const void* hidden, int32_t hidden_dtype, int32_t num_tokens, void* hidden_fp8,

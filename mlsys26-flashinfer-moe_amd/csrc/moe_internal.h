@@ -133,5 +133,6 @@ hipError_t launch_combine(const GemmParams& p, hipStream_t s);
 hipError_t launch_gemm1_tile(const GemmParams& p, int rows_per_item, hipStream_t s);
 hipError_t launch_quantize_hidden(const void* x, int dtype, int T, uint8_t* q, float* scale, hipStream_t s);
 hipError_t launch_gemm2_tile(const GemmParams& p, int rows_per_item, hipStream_t s);
+hipError_t launch_clear_control(int32_t* counters, hipStream_t s);
 
 }  // namespace moe

@@ -68,13 +68,16 @@ class Workspace:
     """A device workspace for the C ABI, initialised once with moe_fp8_workspace_init.
 
     Every dispatch rewrites the control block before the GEMMs read it, so one workspace
-    serves any number of successive calls issued on one stream.
+    serves any number of successive calls issued on one stream. The initialisation is a
+    kernel launch, so a workspace created while its stream is being captured into a graph
+    puts a kernel node (never a memset node) into that graph.
     """
 
     def __init__(self, num_tokens: int, device: torch.device, stream: torch.cuda.Stream | None = None):
         self.layout = _lib.workspace_layout(num_tokens)
         self.nbytes = int(self.layout.total_bytes)
         self.buffer = torch.empty(max(self.nbytes, 256), dtype=torch.uint8, device=device)
+        self.captured = False   # set once a graph capture has recorded a call using it
         stream = stream or torch.cuda.current_stream(device)
         _lib.check(_lib.load().moe_fp8_workspace_init(self.buffer.data_ptr(), self.buffer.numel(),
                                                       stream.cuda_stream), "moe_fp8_workspace_init")
@@ -90,24 +93,57 @@ class Workspace:
         return self.buffer[off:off + nbytes].view(dtype)
 
 
-_ws_lock = threading.Lock()
-_ws_cache: dict[tuple[int, int], Workspace] = {}
+class WorkspaceCache:
+    """One workspace per (device, stream), grown when a call needs more.
+
+    A HIP graph that captured a call keeps that call's workspace pointer. A workspace that a
+    capture has used is therefore never freed: when a larger call on its stream replaces it,
+    it moves to a retired list that lives as long as the process, so that replays of the
+    graph keep writing memory nobody else owns. Workspaces no capture has used are freed when
+    replaced. A workspace created during a capture comes from the graph's memory pool and is
+    kept alive here like any other. Replays and eager calls that share a workspace must not
+    overlap in time: replay a graph on the stream it was captured on, or synchronise.
+
+    `make(num_tokens, device, stream)` creates a workspace and `capturing()` says whether the
+    current stream is being captured; both are injectable so that the policy is testable
+    without a GPU.
+    """
+
+    def __init__(self, make=None, capturing=None):
+        self._make = make or (lambda T, dev, stream: Workspace(T, dev, stream))
+        self._capturing = capturing or torch.cuda.is_current_stream_capturing
+        self._lock = threading.Lock()
+        self._cache = {}
+        self._retired = []
+
+    def get(self, key, num_tokens: int, need_bytes: int, device, stream):
+        with self._lock:
+            ws = self._cache.get(key)
+            if ws is None or ws.buffer.numel() < need_bytes:
+                if ws is not None and ws.captured:
+                    self._retired.append(ws)
+                ws = self._make(num_tokens, device, stream)
+                self._cache[key] = ws
+            elif ws.layout.num_tokens != num_tokens:
+                ws.layout = _lib.workspace_layout(num_tokens)
+                ws.nbytes = int(ws.layout.total_bytes)
+            if self._capturing():
+                ws.captured = True
+            return ws
+
+    @property
+    def retired(self) -> list:
+        return list(self._retired)
+
+
+_workspaces = WorkspaceCache()
 
 
 def workspace_for(num_tokens: int, device: torch.device) -> Workspace:
     """The cached workspace of the current stream on `device`, grown to fit num_tokens."""
     stream = torch.cuda.current_stream(device)
     key = (device.index if device.index is not None else torch.cuda.current_device(), stream.cuda_stream)
-    need = _lib.workspace_bytes(num_tokens)
-    with _ws_lock:
-        ws = _ws_cache.get(key)
-        if ws is None or ws.buffer.numel() < need:
-            ws = Workspace(num_tokens, device, stream)
-            _ws_cache[key] = ws
-        elif ws.layout.num_tokens != num_tokens:
-            ws.layout = _lib.workspace_layout(num_tokens)
-            ws.nbytes = int(ws.layout.total_bytes)
-        return ws
+    return _workspaces.get(key, num_tokens, _lib.workspace_bytes(num_tokens), device, stream)
 
 
 def make_args(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,

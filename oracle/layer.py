@@ -11,9 +11,14 @@ mode="definition": the intermediate C stays fp32 (the definition's math); each t
 mode="emulated":   C is requantised to e4m3 with one scale per row per `requant_block`
   columns before GEMM2 (kernel.py:131-135 uses 64; the HIP kernels use 128), and each
   token sums its weighted rows in top-k slot order starting from 0, as the HIP combine
-  does; a token with one local assignment gets exactly that row.
-Weights are dequantised one touched expert at a time; `tokens` restricts the GEMMs and
-the output to a subset of tokens (routing still runs for all of them).
+  does; a token with one local assignment gets exactly that row. With `act_override`
+  = (act uint8 [N, I], act_scale fp32 [N, I/128]) in bucket-row order, GEMM1 is skipped
+  and GEMM2 + combine run on that intermediate instead of the oracle's own: a check of
+  the second half of the layer on exactly the intermediate a kernel produced.
+Weights are dequantised one touched expert at a time (kept in `dequant_cache`, a dict the
+caller owns, when given, so that several calls on one weight set dequantise each expert
+once); `tokens` restricts the GEMMs and the output to a subset of tokens (routing still
+runs for all of them).
 """
 from __future__ import annotations
 
@@ -27,10 +32,21 @@ from . import routing
 F32 = np.float32
 
 
+def _expert_weights(e, w13q, s13, w2q, s2, block, cache):
+    """fp32 W13[e] and W2[e], dequantised (kernel.py:111-120, :228-232), from `cache` if there."""
+    if cache is not None and e in cache:
+        return cache[e]
+    w = (ex.dequant_blocks(w13q[e], s13[e], block), ex.dequant_blocks(w2q[e], s2[e], block))
+    if cache is not None:
+        cache[e] = w
+    return w
+
+
 def layer_forward(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
                   gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, local_expert_offset,
                   routed_scaling_factor, mode: str = "definition", requant_block: int = 128,
-                  topk=None, tokens=None, block: int = 128):
+                  topk=None, tokens=None, block: int = 128, dequant_cache: dict | None = None,
+                  act_override=None):
     """All arrays are numpy: logits fp32 [T, E], bias fp32 [E], hidden uint8 [T, H],
     hidden scale fp32 [H/128, T], W13 uint8 [E_l, 2I, H], S13 fp32 [E_l, 2I/128, H/128],
     W2 uint8 [E_l, H, I], S2 fp32 [E_l, H/128, I/128]. Returns a dict of intermediates
@@ -38,6 +54,8 @@ def layer_forward(routing_logits, routing_bias, hidden_states, hidden_states_sca
     (all tokens when None)."""
     if mode not in ("definition", "emulated"):
         raise ValueError(mode)
+    if act_override is not None and (mode != "emulated" or requant_block != 128):
+        raise ValueError("act_override needs mode='emulated' with 128-column blocks")
     hidden = np.asarray(hidden_states, dtype=np.uint8)
     T, H = hidden.shape
     e_local, two_i, _ = gemm1_weights.shape
@@ -68,15 +86,19 @@ def layer_forward(routing_logits, routing_bias, hidden_states, hidden_states_sca
             continue
         tok = d["sorted_token"][rows]
         a = ex.dequant_rows(hidden[tok], np.asarray(hidden_states_scale)[:, tok], block)
-        w13 = ex.dequant_blocks(gemm1_weights[e], gemm1_weights_scale[e], block)
-        c = ex.swiglu(ex.gemm(a, w13), inter)
+        w13, w2 = _expert_weights(e, gemm1_weights, gemm1_weights_scale, gemm2_weights,
+                                  gemm2_weights_scale, block, dequant_cache)
+        if act_override is None:
+            c = ex.swiglu(ex.gemm(a, w13), inter)
+            swiglu[rows] = c
         del w13
-        swiglu[rows] = c
         if mode == "emulated":
-            q, sc = ex.requant_rows(c, requant_block)
+            if act_override is None:
+                q, sc = ex.requant_rows(c, requant_block)
+            else:
+                q, sc = act_override[0][rows], act_override[1][rows]
             act[rows], act_scale[rows] = q, sc
             c = ex.dequant_requant(q, sc, requant_block)
-        w2 = ex.dequant_blocks(gemm2_weights[e], gemm2_weights_scale[e], block)
         o = ex.gemm(c, w2)
         del w2
         y[rows] = (o * d["sorted_weight"][rows][:, None]).astype(F32)

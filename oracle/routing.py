@@ -48,13 +48,6 @@ def sigmoid_f32(x: np.ndarray) -> np.ndarray:
 def route(logits: np.ndarray, bias: np.ndarray, routed_scaling_factor: float,
           n_group: int = 8, topk_group: int = 4, top_k: int = 8):
     """Returns (topk_ids int32 [T, top_k] in selection order, topk_weights fp32 [T, top_k])."""
-    ids, weights, _, _ = route_detail(logits, bias, routed_scaling_factor, n_group, topk_group, top_k)
-    return ids, weights
-
-
-def route_detail(logits: np.ndarray, bias: np.ndarray, routed_scaling_factor: float,
-                 n_group: int = 8, topk_group: int = 4, top_k: int = 8):
-    """route() plus the kept-group mask [T, n_group] and the biased scores b [T, E]."""
     logits = np.asarray(logits, dtype=F32)
     bias = np.asarray(bias, dtype=F32).reshape(-1)
     T, E = logits.shape
@@ -88,22 +81,5 @@ def route_detail(logits: np.ndarray, bias: np.ndarray, routed_scaling_factor: fl
         total = (total + svals[:, k]).astype(F32)
     total = (total + F32(1e-20)).astype(F32)
     weights = ((svals / total[:, None]).astype(F32) * F32(routed_scaling_factor)).astype(F32)
-    return ids, weights, selected, b
+    return ids, weights
 
-
-def selection_margins(logits: np.ndarray, bias: np.ndarray, n_group: int = 8, topk_group: int = 4,
-                      top_k: int = 8):
-    """Per token: (gap between the kept and the first dropped group score, gap between the
-    k-th and (k+1)-th biased score inside the kept groups). A token whose gaps are tiny is
-    a near-tie, for which any fp32 implementation of the sigmoid may legitimately choose
-    differently."""
-    _, _, selected, b = route_detail(logits, bias, 1.0, n_group, topk_group, top_k)
-    T, E = b.shape
-    gsz = E // n_group
-    srt = np.sort(b.reshape(T, n_group, gsz), axis=-1)
-    gs = np.sort(srt[..., -1] + srt[..., -2], axis=1)[:, ::-1]
-    group_gap = gs[:, topk_group - 1] - gs[:, topk_group]
-    kept = np.where(np.repeat(selected, gsz, axis=1), b, -np.inf)
-    ks = np.sort(kept, axis=1)[:, ::-1]
-    expert_gap = ks[:, top_k - 1] - ks[:, top_k]
-    return group_gap, expert_gap

@@ -108,6 +108,13 @@ def test_argument_errors_are_reported_before_any_launch(pkg, lib):
     a = _args(pkg)
     a.output_dtype = 2
     assert lib.moe_fp8_gemm2_combine(ctypes.byref(a), 0x1000, big, None) == L.EINVAL_OUT_DTYPE
+    # the evented variant: all four events are required, and argument errors come first
+    a = _args(pkg)
+    ev = (ctypes.c_void_p * 4)(0x10, 0x20, 0x30, 0x40)
+    assert lib.moe_fp8_run_profiled(ctypes.byref(a), 0x1000, big, None, None) == L.EINVAL_POINTER
+    assert lib.moe_fp8_run_profiled(ctypes.byref(a), 0x1000, big, None,
+                                    (ctypes.c_void_p * 4)(0x10, 0x20, None, 0x40)) == L.EINVAL_POINTER
+    assert lib.moe_fp8_run_profiled(ctypes.byref(a), 0x1000, big - 1, None, ev) == L.EWORKSPACE
     # T = 0 is a no-op that succeeds without a device
     a = _args(pkg, 0)
     assert lib.moe_fp8_run(ctypes.byref(a), None, 0, None) == L.OK

@@ -61,3 +61,93 @@ def test_graph_replays_match_eager(T):
     g.replay()
     torch.cuda.synchronize()
     assert torch.equal(out_graph, ref2)
+
+
+def _kw(gh, T, seed, w):
+    dev = torch.device("cuda:0")
+    logits, bias, hq, hs = gh.inputs.make_activations(T, seed, dev)
+    return dict(routing_logits=logits, routing_bias=bias, hidden_states=hq, hidden_states_scale=hs,
+                gemm1_weights=w[0], gemm1_weights_scale=w[1], gemm2_weights=w[2], gemm2_weights_scale=w[3],
+                local_expert_offset=0, routed_scaling_factor=2.5)
+
+
+def _eager_on(stream, gh, kw, T):
+    dev = torch.device("cuda:0")
+    out = torch.empty((T, 7168), dtype=torch.bfloat16, device=dev)
+    stream.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(stream):
+        gh.pkg.run(**kw, output=out)
+    stream.synchronize()
+    return out
+
+
+def test_first_call_under_capture():
+    """run() called for the first time inside torch.cuda.graph (its own capture stream, on which
+    no call has run before): the workspace is allocated and initialised inside the capture by a
+    kernel, and every replay equals an eager call."""
+    gh = _gh()
+    dev = torch.device("cuda:0")
+    T = 24
+    w = gh.inputs.make_weights(4100, dev)
+    kw = _kw(gh, T, 4101, w)
+    ref = _eager_on(torch.cuda.Stream(dev), gh, kw, T)
+    out = torch.empty((T, 7168), dtype=torch.bfloat16, device=dev)
+    g = torch.cuda.CUDAGraph()
+    torch.cuda.synchronize()
+    print("capture of a first call, T=24", flush=True)
+    from mlsys26_flashinfer_moe_amd import moe
+    saved = moe._workspaces
+    moe._workspaces = moe.WorkspaceCache()      # no stream has a workspace yet
+    try:
+        with torch.cuda.graph(g):   # torch's own capture stream
+            gh.pkg.run(**kw, output=out)
+    finally:
+        moe._workspaces, fresh = saved, moe._workspaces
+    assert len(fresh._cache) == 1 and next(iter(fresh._cache.values())).captured
+    for rep in range(3):
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), f"replay {rep} differs from the eager result"
+        _ = (torch.randn(1 << 20, device=dev) * 2).sum().item()
+
+
+def test_replay_after_a_larger_eager_call_on_the_capture_stream():
+    """A graph captured at T=32 on stream s keeps its workspace when an eager call of T=700 on s
+    needs a larger one: the replay still equals the T=32 eager result, and the T=700 call's
+    result is unchanged by the replay."""
+    from mlsys26_flashinfer_moe_amd import moe
+    gh = _gh()
+    dev = torch.device("cuda:0")
+    w = gh.inputs.make_weights(4200, dev)
+    s = torch.cuda.Stream(dev)
+    small, big = _kw(gh, 32, 4201, w), _kw(gh, 700, 4202, w)
+    saved = moe._workspaces
+    moe._workspaces = moe.WorkspaceCache()      # a fresh cache: s (a pooled stream) has no workspace yet
+    try:
+        _capture_then_grow(gh, moe, dev, s, small, big)
+    finally:
+        moe._workspaces = saved
+
+
+def _capture_then_grow(gh, moe, dev, s, small, big):
+    ref_small = _eager_on(s, gh, small, 32)     # creates the T=32 workspace of s
+    out = torch.empty((32, 7168), dtype=torch.bfloat16, device=dev)
+    g = torch.cuda.CUDAGraph()
+    torch.cuda.synchronize()
+    print("capture at T=32, then an eager T=700 call on the same stream", flush=True)
+    with torch.cuda.graph(g, stream=s):
+        gh.pkg.run(**small, output=out)
+    n_retired = len(moe._workspaces.retired)
+    ref_big = _eager_on(s, gh, big, 700)        # replaces the workspace of s
+    assert len(moe._workspaces.retired) == n_retired + 1, "the captured workspace was not retained"
+    for rep in range(2):
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        with torch.cuda.stream(s):
+            g.replay()
+        s.synchronize()
+        assert torch.equal(out, ref_small), f"replay {rep} differs from the eager result"
+        again = _eager_on(s, gh, big, 700)
+        assert torch.equal(again, ref_big)

@@ -1,16 +1,29 @@
 """GPU parity of the whole layer (routing through combine) against the CPU oracle.
 
-Tolerances (bf16 output, compared as float32):
-  vs the emulated oracle (same fp8 requantisation of the SwiGLU output as the kernels,
-  1x128 blocks): |gpu - ref| <= 0.02 + 0.02 |ref| element-wise and relative RMS <= 0.01;
-  the residual comes from fp32 summation order, which flips a few fp8 roundings of the
-  intermediate (for constructed top-k lists the 0.02 grows as sqrt(max local experts per
-  token / 2), since every local expert adds its own flips);
-  vs the definition (fp32 intermediate, kernel.py's math without requantisation):
-  |gpu - ref| <= 0.25 + 0.1 |ref| element-wise and relative RMS <= 0.05.
-Sizes: T from 1 to 32768 (the largest puts parked GEMM2 rows beyond 2 GiB of the workspace).
-The fp8 intermediate itself: its scales within 3e-4 relative, and at most 1 code step
-apart on at most 1% of the bytes.
+The layer is checked in two halves and as a whole, on bf16 output compared as float32:
+  * GEMM1 + SwiGLU + requantisation, through the fp8 intermediate it leaves in the
+    workspace, against the emulated oracle (the kernels' algorithm: 1x128 requantisation):
+    scales within 3e-4 relative, at most 1% of the bytes different, each by at most one
+    fp8 step (plus 4e-4 of the row maximum for the MFMA's block-sum precision).
+  * GEMM2 + weighted combine, on exactly that intermediate (the oracle's act_override):
+    |gpu - oracle| <= 2^-7 |oracle| + 4e-4 max_row |oracle| element-wise, i.e. one bf16
+    rounding step plus the block-sum precision. No fp8 rounding can differ here, so the
+    bound is tight: a wrong weight, slot or scale moves elements by far more.
+  * The whole layer against the emulated oracle's own intermediate: relative RMS <= 0.01.
+    (Element-wise this comparison is not a fixed bound: where the two fp32 GEMM1 sums of a
+    value at the top of the fp8 range round to different codes, 7% of that block's maximum,
+    every element of the token's output row moves by a few hundredths.)
+  * The whole layer against the definition (fp32 intermediate, kernel.py's math without
+    requantisation): relative RMS <= 0.05; and against the reference's own algorithm, which
+    requantises per 64 columns (kernel.py:131-135) where these kernels use 128, per token
+        max_j |gpu - def| <= 2 * max_j |ref64 - def| + 1/64,
+    and over all checked elements rms(gpu - def) <= 1.25 * rms(ref64 - def). The factor 2:
+    on the CPU the 128-column algorithm's per-token maximum reaches 1.56x the 64-column
+    one's (median 1.09x; t16, t64 and t1024_off64, every token), and the GPU's summation
+    order adds its fp8 flips on top (measured up to 1.43x at T=8192 and the skewed T=4096
+    batch, 256 tokens each); 1/64 is four bf16 steps at the output's typical magnitude.
+Sizes: T from 1 to 32768 (the largest puts parked GEMM2 rows beyond 2 GiB of the workspace);
+T=8192 and the skewed T=4096 batch are checked on 256 sampled tokens each.
 """
 import numpy as np
 import pytest
@@ -42,6 +55,7 @@ def _weights():
         _WEIGHTS["w"] = w
         _WEIGHTS["np"] = tuple(t.view(torch.uint8).cpu().numpy() if t.dtype == torch.float8_e4m3fn
                                else t.cpu().numpy() for t in w)
+        _WEIGHTS["cache"] = {}   # the oracle's dequantised experts of this weight set
     return _WEIGHTS["w"], _WEIGHTS["np"]
 
 
@@ -62,16 +76,8 @@ def _workload(name):
         kw = gh.inputs.make_workload(name, dev, weights=w)
     npkw = gh.to_numpy_inputs({**kw, "gemm1_weights": w[0][:1], "gemm2_weights": w[2][:1]})
     npkw["gemm1_weights"], npkw["gemm1_weights_scale"], npkw["gemm2_weights"], npkw["gemm2_weights_scale"] = wnp
+    npkw["dequant_cache"] = _WEIGHTS["cache"]
     return kw, npkw
-
-
-def _compare(got, ref, atol, rtol, rms_rel, what):
-    err = np.abs(got - ref)
-    bad = err > atol + rtol * np.abs(ref)
-    rms = np.sqrt(np.mean((got - ref) ** 2)) / max(np.sqrt(np.mean(ref ** 2)), 1e-30)
-    print(f"{what}: max err {err.max():.4g}, rel rms {rms:.4g}, violations {bad.sum()}", flush=True)
-    assert not bad.any(), f"{what}: {bad.sum()} elements outside tolerance, max err {err.max():.4g}"
-    assert rms <= rms_rel, f"{what}: relative RMS {rms:.4g} > {rms_rel}"
 
 
 def _run_full(kw, out_dtype=torch.bfloat16):
@@ -83,9 +89,57 @@ def _run_full(kw, out_dtype=torch.bfloat16):
     return out
 
 
+def _read_act(ws, n):
+    gh = _gh()
+    act = gh.read(ws, "act", torch.uint8, n * 2048).reshape(n, 2048)
+    sc = gh.read(ws, "act_scale", torch.float32, n * 16).reshape(n, 16)
+    return act, sc
+
+
+def _check_intermediate(act, sc, emu, rows, what):
+    """The GPU's fp8 intermediate (bucket rows `rows`) against the emulated oracle's."""
+    a, s, ra, rs = act[rows], sc[rows], emu["act"][rows], emu["act_scale"][rows]
+    # The fp8 MFMA sums each 128-long K block at less than fp32 precision (observed
+    # relative differences of the row maxima up to ~6e-5), so the scales agree to 3e-4.
+    np.testing.assert_allclose(s, rs, rtol=3e-4, atol=0)
+    diff = a != ra
+    print(f"{what}: act bytes differing {np.mean(diff):.4%}", flush=True)
+    assert np.mean(diff) <= 0.01
+    # Dequantised, the two intermediates differ by at most one fp8 step (12.5% of the
+    # value) plus the accumulation difference, which is absolute: 4e-4 of the row maximum.
+    deq_g = ofp8.decode(a) * np.repeat(s, 128, axis=1)
+    deq_r = ofp8.decode(ra) * np.repeat(rs, 128, axis=1)
+    row_max = 448.0 * np.repeat(rs, 128, axis=1)
+    err = np.abs(deq_g - deq_r)
+    bound = 0.125 * np.abs(deq_r) + 4e-4 * row_max
+    print(f"{what}: intermediate max err / bound {np.max(err / bound, initial=0):.3f}", flush=True)
+    assert np.all(err <= bound)
+
+
+def _check_second_half(got, npkw, act, sc, tokens, what, topk=None):
+    """GEMM2 + combine on the GPU's own intermediate: one bf16 step + block-sum precision."""
+    ref = olayer.layer_forward(**npkw, mode="emulated", tokens=tokens, topk=topk, act_override=(act, sc))["output"]
+    row_max = np.max(np.abs(ref), axis=1, keepdims=True)
+    err = np.abs(got - ref)
+    bound = 2.0 ** -7 * np.abs(ref) + 4e-4 * row_max
+    print(f"{what}: GEMM2 + combine on the GPU intermediate, max err / bound "
+          f"{np.max(err / np.maximum(bound, 1e-30), initial=0):.3f}", flush=True)
+    assert np.all(err <= bound), f"{what}: {int(np.sum(err > bound))} elements beyond one bf16 step"
+
+
+def _wanted_rows(emu, tokens):
+    """Bucket rows whose token is among `tokens` (all rows when None)."""
+    st = emu["sorted_token"]
+    if tokens is None:
+        return np.arange(len(st))
+    return np.where(np.isin(st, tokens))[0]
+
+
 @pytest.mark.parametrize("name,sample", [("t16", None), ("t64", None), ("t256", None), ("t1024_off64", None),
-                                         ("t8192", 40), ("t4096_skew", 24), ("t32768", 24)])
+                                         ("t8192", 256), ("t4096_skew", 256), ("t32768", 24)])
 def test_layer_matches_oracle(name, sample):
+    from mlsys26_flashinfer_moe_amd import moe
+    gh = _gh()
     kw, npkw = _workload(name)
     T = kw["routing_logits"].shape[0]
     print(f"layer {name} T={T}", flush=True)
@@ -96,18 +150,36 @@ def test_layer_matches_oracle(name, sample):
     if sample is not None:
         rng = np.random.default_rng(T)
         tokens = np.sort(rng.choice(T, sample, replace=False))
-    emu = olayer.layer_forward(**npkw, mode="emulated", tokens=tokens)
     sel = slice(None) if tokens is None else tokens
-    _compare(got[sel], emu["output"], 0.02, 0.02, 0.01, f"{name} vs emulated oracle")
-    ref = olayer.layer_forward(**npkw, mode="definition", tokens=tokens)
-    _compare(got[sel], ref["output"], 0.25, 0.1, 0.05, f"{name} vs definition")
-    # The fp8 requantisation of the SwiGLU output is the reference's own algorithm
-    # (kernel.py:131-135, 64-column blocks); the layer must not be further from the fp32
-    # definition than that algorithm is.
-    ref64 = olayer.layer_forward(**npkw, mode="emulated", requant_block=64, tokens=tokens)
+    g = got[sel]
+    emu = olayer.layer_forward(**npkw, mode="emulated", tokens=tokens)
+    n = len(emu["sorted_slot"])
+    ws = moe.workspace_for(T, kw["routing_logits"].device)   # the workspace run() used
+    assert gh.counters(ws)[1] == n
+    act, sc = _read_act(ws, n)
+    _check_intermediate(act, sc, emu, _wanted_rows(emu, tokens), name)
+    _check_second_half(g, npkw, act, sc, tokens, name)
     rms = lambda x: float(np.sqrt(np.mean(np.square(x))))
-    e_gpu = rms(got[sel] - ref["output"])
-    e_ref = rms(ref64["output"] - ref["output"])
+    rel = rms(g - emu["output"]) / max(rms(emu["output"]), 1e-30)
+    print(f"{name} vs emulated oracle: rel rms {rel:.4g}, max err {np.max(np.abs(g - emu['output'])):.4g}", flush=True)
+    assert rel <= 0.01
+    ref = olayer.layer_forward(**npkw, mode="definition", tokens=tokens)["output"]
+    rel = rms(g - ref) / max(rms(ref), 1e-30)
+    print(f"{name} vs definition: rel rms {rel:.4g}", flush=True)
+    assert rel <= 0.05
+    # the reference's own algorithm (64-column requantisation, kernel.py:131-135): per token
+    # and in aggregate, the layer is no further from the fp32 definition than it, within the
+    # factors stated at the top of this file
+    ref64 = olayer.layer_forward(**npkw, mode="emulated", requant_block=64, tokens=tokens)["output"]
+    tok_gpu = np.max(np.abs(g - ref), axis=1)
+    tok_ref = np.max(np.abs(ref64 - ref), axis=1)
+    ratio = tok_gpu / np.maximum(tok_ref, 1e-30)
+    live = tok_ref > 0
+    print(f"{name}: per-token max|gpu - def| / max|ref64 - def|: max {np.max(ratio[live], initial=0):.3f}, "
+          f"median {np.median(ratio[live]) if live.any() else 0:.3f} over {int(live.sum())} tokens", flush=True)
+    bad = tok_gpu > 2.0 * tok_ref + 1.0 / 64
+    assert not bad.any(), f"{name}: {int(bad.sum())} tokens beyond 2 x the reference algorithm's error"
+    e_gpu, e_ref = rms(g - ref), rms(ref64 - ref)
     print(f"{name}: rms(gpu - definition) {e_gpu:.4g}, rms(reference algorithm - definition) {e_ref:.4g}",
           flush=True)
     assert e_gpu <= 1.25 * e_ref
@@ -180,23 +252,8 @@ def test_intermediate_fp8_matches_oracle(name):
         print(f"{name}: swiglu max err / bound {np.max(err / bound):.3f}", flush=True)
         assert np.all(err <= bound)
     gh.gemm2_combine(args, ws)
-    act = gh.read(ws, "act", torch.uint8, n * 2048).reshape(n, 2048)
-    sc = gh.read(ws, "act_scale", torch.float32, n * 16).reshape(n, 16)
-    # The fp8 MFMA sums each 128-long K block at less than fp32 precision (observed
-    # relative differences of the row maxima up to ~6e-5), so the scales agree to 3e-4.
-    np.testing.assert_allclose(sc, emu["act_scale"], rtol=3e-4, atol=0)
-    diff = act != emu["act"]
-    print(f"{name}: act bytes differing {np.mean(diff):.4%}", flush=True)
-    assert np.mean(diff) <= 0.01
-    # Dequantised, the two intermediates differ by at most one fp8 step (12.5% of the
-    # value) plus the accumulation difference, which is absolute: 4e-4 of the row maximum.
-    deq_g = ofp8.decode(act) * np.repeat(sc, 128, axis=1)
-    deq_r = ofp8.decode(emu["act"]) * np.repeat(emu["act_scale"], 128, axis=1)
-    row_max = 448.0 * np.repeat(emu["act_scale"], 128, axis=1)
-    err = np.abs(deq_g - deq_r)
-    bound = 0.125 * np.abs(deq_r) + 4e-4 * row_max
-    print(f"{name}: max err / bound {np.max(err / bound):.3f}", flush=True)
-    assert np.all(err <= bound)
+    act, sc = _read_act(ws, n)
+    _check_intermediate(act, sc, emu, np.arange(n), name)
 
 
 @pytest.mark.parametrize("name", ["t1024_off64", "t4096_skew"])
@@ -301,6 +358,7 @@ def test_layer_edge_cases_given_topk(T, case):
     assert np.isfinite(got).all()
     npkw = gh.to_numpy_inputs({**kw, "gemm1_weights": w[0][:1], "gemm2_weights": w[2][:1]})
     npkw["gemm1_weights"], npkw["gemm1_weights_scale"], npkw["gemm2_weights"], npkw["gemm2_weights_scale"] = wnp
+    npkw["dequant_cache"] = _WEIGHTS["cache"]
     tokens = None if T <= 40 else np.sort(rng.choice(T, 24, replace=False))
     if case == "few_local":   # every kind of token: 2 local experts, each item's edges, none
         tokens = np.unique(np.concatenate([tokens, [0, 39, 40, 299, 300, 459, 460, 479, 480, 639, 640, T - 1]]))
@@ -309,12 +367,15 @@ def test_layer_edge_cases_given_topk(T, case):
     if case == "none_local":
         assert np.all(got == 0)
         return
-    # Each output element sums one contribution per local expert, and each carries the fp8
-    # rounding flips of its intermediate; with up to 8 local experts per token the element-wise
-    # bound grows with the square root of that count (the relative RMS bound does not).
-    nloc = int(np.max(np.sum(ids[sel] < 32, axis=1)))
-    atol = 0.02 * float(np.sqrt(max(1.0, nloc / 2.0)))
-    _compare(got[sel], emu["output"], atol, 0.02, 0.01, f"T={T} {case} vs emulated oracle")
+    what = f"T={T} {case}"
+    n = len(emu["sorted_slot"])
+    act, sc = _read_act(ws, n)
+    _check_intermediate(act, sc, emu, _wanted_rows(emu, tokens), what)
+    _check_second_half(got[sel], npkw, act, sc, tokens, what, topk=(ids, tw))
+    g, r = got[sel], emu["output"]
+    rel = np.sqrt(np.mean((g - r) ** 2)) / max(np.sqrt(np.mean(r ** 2)), 1e-30)
+    print(f"{what} vs emulated oracle: rel rms {rel:.4g}", flush=True)
+    assert rel <= 0.01
     if case == "few_local":
         assert ws.layout.rows_per_item == 160
         assert np.all(got[640:] == 0)
@@ -334,9 +395,16 @@ def test_layer_last_expert_group():
     got = _run_full(kw).float().cpu().numpy()
     npkw = gh.to_numpy_inputs({**kw, "gemm1_weights": w[0][:1], "gemm2_weights": w[2][:1]})
     npkw["gemm1_weights"], npkw["gemm1_weights_scale"], npkw["gemm2_weights"], npkw["gemm2_weights_scale"] = wnp
+    npkw["dequant_cache"] = _WEIGHTS["cache"]
     emu = olayer.layer_forward(**npkw, mode="emulated")
     assert emu["token_nlocal"].sum() > 0
-    _compare(got, emu["output"], 0.02, 0.02, 0.01, "offset 224 vs emulated oracle")
+    from mlsys26_flashinfer_moe_amd import moe
+    n = len(emu["sorted_slot"])
+    act, sc = _read_act(moe.workspace_for(T, dev), n)
+    _check_intermediate(act, sc, emu, np.arange(n), "offset 224")
+    _check_second_half(got, npkw, act, sc, None, "offset 224")
+    rel = np.sqrt(np.mean((got - emu["output"]) ** 2)) / max(np.sqrt(np.mean(emu["output"] ** 2)), 1e-30)
+    assert rel <= 0.01, f"offset 224 vs emulated oracle: rel rms {rel:.4g}"
 
 
 def test_zero_tokens():

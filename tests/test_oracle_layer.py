@@ -98,3 +98,33 @@ def test_tokens_subset_gives_the_same_rows():
     full = olayer.layer_forward(**kw, mode="definition", topk=topk)
     sub = olayer.layer_forward(**kw, mode="definition", topk=topk, tokens=np.array([0, 3]))
     assert np.array_equal(sub["output_f32"], full["output_f32"][[0, 3]])
+
+
+def test_dequant_cache_gives_the_same_result():
+    """A shared dequantisation cache across calls and modes changes no bit of the output."""
+    kw, topk = _inputs(5, 4)
+    cache = {}
+    for mode in ("definition", "emulated"):
+        plain = olayer.layer_forward(**kw, mode=mode, topk=topk)
+        cached = olayer.layer_forward(**kw, mode=mode, topk=topk, dequant_cache=cache)
+        assert np.array_equal(plain["output_f32"], cached["output_f32"])
+    assert len(cache) > 0
+
+
+def test_act_override_reproduces_emulated_mode():
+    """GEMM2 + combine on a given intermediate: fed the emulated mode's own fp8 intermediate,
+    the result is bit-identical; a changed intermediate byte changes the output of (only) the
+    tokens whose rows use it."""
+    kw, topk = _inputs(5, 5)
+    ref = olayer.layer_forward(**kw, mode="emulated", topk=topk)
+    act, sc = ref["act"].copy(), ref["act_scale"].copy()
+    got = olayer.layer_forward(**kw, mode="emulated", topk=topk, act_override=(act, sc))
+    assert np.array_equal(got["output_f32"], ref["output_f32"])
+    row = 0
+    tok = int(ref["sorted_token"][row])
+    act[row, 3] ^= 0x01                          # one code step
+    moved = olayer.layer_forward(**kw, mode="emulated", topk=topk, act_override=(act, sc))
+    diff = np.any(moved["output_f32"] != ref["output_f32"], axis=1)
+    assert diff[tok] and diff.sum() == 1
+    with pytest.raises(ValueError):
+        olayer.layer_forward(**kw, mode="definition", topk=topk, act_override=(act, sc))
