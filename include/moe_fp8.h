@@ -68,6 +68,7 @@ extern "C" {
 #define MOE_FP8_ELAUNCH            -6  /* a HIP launch failed (hipGetLastError) */
 #define MOE_FP8_EDEVICE            -7  /* current device is not gfx950 */
 #define MOE_FP8_EINVAL_HIDDEN_DTYPE -8 /* hidden_dtype of moe_fp8_quantize_hidden unknown */
+#define MOE_FP8_ESTATIC_TOKENS     -9  /* num_tokens > MOE_FP8_STATIC_MAX_TOKENS (moe_fp8_run_static) */
 
 /* Largest num_tokens accepted: keeps every flat index (T*8*7168) inside int64 and
  * the per-token slot index inside int32. */
@@ -177,6 +178,22 @@ int moe_fp8_run(const moe_fp8_args* args, void* workspace, size_t workspace_byte
  * (:649-693) and GEMM2 + finalize (:695-729) sections. */
 int moe_fp8_run_profiled(const moe_fp8_args* args, void* workspace, size_t workspace_bytes,
                          hipStream_t stream, hipEvent_t events[4]);
+
+/* moe_fp8_run without a caller workspace, for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). No
+ * counterpart in the reference, whose temporaries come from torch's allocator
+ * (kernel.py:348-370, 629-630, 669-670, 704). The workspace is a device array inside the
+ * library of MOE_FP8_STATIC_SCRATCH_BYTES (20 MiB), one per GPU that loads the library, held
+ * until the process ends; it holds the workspace of up to MOE_FP8_STATIC_MAX_TOKENS (64)
+ * tokens, and larger batches return MOE_FP8_ESTATIC_TOKENS without launching anything.
+ * Nothing is allocated or freed by this call (the first call on a device resolves the
+ * array's address and clears its control block with a kernel). Every call on one GPU shares
+ * that GPU's array: calls that overlap in time on one GPU (on different streams, or from
+ * different threads without ordering) race and give wrong results; calls ordered on one
+ * stream are safe, each rewriting what it reads. Results are bit-identical to moe_fp8_run. */
+#define MOE_FP8_STATIC_MAX_TOKENS    64
+#define MOE_FP8_STATIC_SCRATCH_BYTES (20u << 20)
+int moe_fp8_run_static(const moe_fp8_args* args, hipStream_t stream);
 
 /* Stage 1: routing and dispatch. Writes topk_ids/topk_weights, the expert histogram,
  * CSR offsets, sorted permutation and the GEMM work list. With skip_routing != 0 the

@@ -39,6 +39,9 @@ EINVAL_OUT_DTYPE = -5
 ELAUNCH = -6
 EDEVICE = -7
 EINVAL_HIDDEN_DTYPE = -8
+ESTATIC_TOKENS = -9
+STATIC_MAX_TOKENS = 64
+STATIC_SCRATCH_BYTES = 20 << 20
 
 EXPORTED_SYMBOLS = (
     "moe_fp8_workspace_bytes",
@@ -46,6 +49,7 @@ EXPORTED_SYMBOLS = (
     "moe_fp8_workspace_init",
     "moe_fp8_run",
     "moe_fp8_run_profiled",
+    "moe_fp8_run_static",
     "moe_fp8_route_dispatch",
     "moe_fp8_gemm1",
     "moe_fp8_gemm2_combine",
@@ -134,6 +138,8 @@ def load() -> ctypes.CDLL:
         lib.moe_fp8_run.restype = ctypes.c_int
         lib.moe_fp8_run_profiled.argtypes = [args_p, vp, sz, vp, ctypes.POINTER(vp)]
         lib.moe_fp8_run_profiled.restype = ctypes.c_int
+        lib.moe_fp8_run_static.argtypes = [args_p, vp]
+        lib.moe_fp8_run_static.restype = ctypes.c_int
         lib.moe_fp8_route_dispatch.argtypes = [args_p, i32, vp, sz, vp]
         lib.moe_fp8_route_dispatch.restype = ctypes.c_int
         lib.moe_fp8_gemm1.argtypes = [args_p, vp, sz, vp]

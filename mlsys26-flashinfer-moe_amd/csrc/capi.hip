@@ -2,6 +2,8 @@
 // run() in kernel.py:562-729 is the interface these entry points replace.
 #include <string.h>
 
+#include <mutex>
+
 #include "moe_internal.h"
 
 namespace moe {
@@ -187,6 +189,35 @@ int run_layer(const moe_fp8_args* args, void* workspace, size_t workspace_bytes,
   return MOE_FP8_OK;
 }
 
+// The workspace of moe_fp8_run_static: device memory the library holds itself, one copy per
+// GPU that loads the library, for callers that cannot allocate. In host code `scratch` names a
+// host-side stand-in, not device memory: its device address comes from hipGetSymbolAddress,
+// once per device (StaticScratch), and only that address is ever passed to kernels.
+__device__ __align__(256) uint8_t scratch[MOE_FP8_STATIC_SCRATCH_BYTES];
+
+struct StaticScratch {
+  std::mutex lock;
+  void* ptr[64] = {};   // device address of `scratch` on each device; null until set up
+};
+StaticScratch g_static;
+
+// The current device's scratch address. The first call on a device resolves it (with that
+// device current) and clears its control block with a kernel on `stream`; every later call's
+// dispatch rewrites the control block before a GEMM reads it.
+int static_scratch(hipStream_t stream, void** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return MOE_FP8_EDEVICE;
+  std::lock_guard<std::mutex> guard(g_static.lock);
+  if (!g_static.ptr[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return MOE_FP8_ELAUNCH;
+    if (launch_clear_control(static_cast<int32_t*>(p), stream) != hipSuccess) return MOE_FP8_ELAUNCH;
+    g_static.ptr[dev] = p;
+  }
+  *out = g_static.ptr[dev];
+  return MOE_FP8_OK;
+}
+
 }  // namespace
 }  // namespace moe
 
@@ -254,6 +285,19 @@ int moe_fp8_run_profiled(const moe_fp8_args* args, void* workspace, size_t works
   return run_layer(args, workspace, workspace_bytes, stream, events);
 }
 
+int moe_fp8_run_static(const moe_fp8_args* args, hipStream_t stream) {
+  if (!args) return MOE_FP8_EINVAL_POINTER;
+  if (args->num_tokens < 0) return MOE_FP8_EINVAL_TOKENS;
+  if (args->num_tokens > MOE_FP8_STATIC_MAX_TOKENS) return MOE_FP8_ESTATIC_TOKENS;
+  if (args->num_tokens == 0) return MOE_FP8_OK;
+  int rc = check_device();
+  if (rc != MOE_FP8_OK) return rc;
+  void* ws = nullptr;
+  rc = static_scratch(stream, &ws);
+  if (rc != MOE_FP8_OK) return rc;
+  return run_layer(args, ws, MOE_FP8_STATIC_SCRATCH_BYTES, stream, nullptr);
+}
+
 int moe_fp8_quantize_hidden(const void* hidden, int32_t hidden_dtype, int32_t num_tokens, void* hidden_fp8,
                             float* hidden_scale, hipStream_t stream) {
   if (num_tokens < 0 || num_tokens > MOE_FP8_MAX_TOKENS) return MOE_FP8_EINVAL_TOKENS;
@@ -279,6 +323,9 @@ const char* moe_fp8_strerror(int code) {
     case MOE_FP8_ELAUNCH: return "a HIP kernel launch failed";
     case MOE_FP8_EDEVICE: return "the current HIP device is not a gfx950 (MI355X) GPU";
     case MOE_FP8_EINVAL_HIDDEN_DTYPE: return "hidden_dtype must be MOE_FP8_HIDDEN_F32, _BF16 or _F16";
+    case MOE_FP8_ESTATIC_TOKENS:
+      return "num_tokens exceeds MOE_FP8_STATIC_MAX_TOKENS (64), the largest batch moe_fp8_run_static's "
+             "built-in workspace holds; use moe_fp8_run with a caller workspace";
     default: return "unknown error code";
   }
 }
