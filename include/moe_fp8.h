@@ -117,7 +117,8 @@ typedef struct moe_fp8_args {
  *                 The parity tests bound the output's distance from fp32 math by that of the
  *                 64-column algorithm (per token at most 2x its maximum error + 1/64).
  *   partial       fp32  [T*8, 7168]      weighted GEMM2 rows of tokens with more than one local
- *                                        assignment, indexed by flat slot             (kernel.py:704)
+ *                                        assignment, indexed by flat slot, above 64 tokens (up to
+ *                                        64 the combine happens inside GEMM2)         (kernel.py:704)
  *   swiglu        fp32  [N_max, 2048]    SwiGLU output before requantisation; only for
  *                                        T <= 512 (0 bytes otherwise)
  */
@@ -215,7 +216,8 @@ int moe_fp8_gemm1(const moe_fp8_args* args, void* workspace, size_t workspace_by
 
 /* Stage 3: (when layout.rows_per_item <= 32) requantisation of the fp32 SwiGLU rows to
  * act/act_scale; GEMM2 of act against the expert's down projection, weighting by the
- * routing weight and the deterministic per-token combine into args->output.
+ * routing weight and the deterministic per-token combine into args->output (up to 64 tokens
+ * in one kernel, above that a separate combine pass over the parked rows).
  * Replaces moe_gemm2_kernel and the finalize copy (kernel.py:695-729, 153-250). */
 int moe_fp8_gemm2_combine(const moe_fp8_args* args, void* workspace, size_t workspace_bytes,
                           hipStream_t stream);

@@ -185,7 +185,7 @@ int run_layer(const moe_fp8_args* args, void* workspace, size_t workspace_bytes,
   }
   if (launch_requant(gp, L.rows_per_item, stream) != hipSuccess) return MOE_FP8_ELAUNCH;
   if (launch_gemm2(gp, L.rows_per_item, stream) != hipSuccess) return MOE_FP8_ELAUNCH;
-  if (launch_combine(gp, stream) != hipSuccess || !mark(3)) return MOE_FP8_ELAUNCH;
+  if (launch_combine(gp, L.rows_per_item, stream) != hipSuccess || !mark(3)) return MOE_FP8_ELAUNCH;
   return MOE_FP8_OK;
 }
 
@@ -270,7 +270,7 @@ int moe_fp8_gemm2_combine(const moe_fp8_args* args, void* workspace, size_t work
   const GemmParams p = gemm_params(args, L, workspace);
   if (launch_requant(p, L.rows_per_item, stream) != hipSuccess) return MOE_FP8_ELAUNCH;
   if (launch_gemm2(p, L.rows_per_item, stream) != hipSuccess) return MOE_FP8_ELAUNCH;
-  return launch_combine(p, stream) == hipSuccess ? MOE_FP8_OK : MOE_FP8_ELAUNCH;
+  return launch_combine(p, L.rows_per_item, stream) == hipSuccess ? MOE_FP8_OK : MOE_FP8_ELAUNCH;
 }
 
 

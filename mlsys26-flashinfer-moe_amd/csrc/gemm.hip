@@ -15,6 +15,9 @@
 //          (kernel.py:236-237); a token with one local assignment gets v written straight
 //          to its output row, the others park v in `partial` by flat slot for
 //          combine_kernel (the reference adds with fp32 atomics, kernel.py:246-250).
+//          Up to 64 tokens GEMM2 and the combine are one kernel instead, gemm2_slice_kernel
+//          (below): a work-group per 32 hidden rows across all items, with the tokens'
+//          weighted sums kept in LDS.
 // A wavefront streams its weight rows and the item's activation rows into a register ring
 // (the next K-step in flight while the current one computes). Every K-step is exactly one 128x128 scale block:
 // one v_mfma_f32_16x16x128_f8f6f4 per fragment pair, then acc += mfma * (s_act * s_w) in
@@ -399,6 +402,141 @@ __global__ __launch_bounds__(256) void requant_kernel(GemmParams p) {
   }
 }
 
+// Decode batches of up to kFusedDispatchTokens tokens (16-row items): GEMM2 and the combine in
+// one kernel, with no fp32 rows parked in `partial`. A work-group owns 32 hidden rows of W2
+// (two MFMA fragments; 224 slices) across every work item, and its wavefront q owns K-steps
+// [4q, 4q+4) of each: per item, q streams the expert's 32 x 512 weight bytes and the item's
+// act rows through a register ring, scales each 128-wide block product (kernel.py:234),
+// weights it by the routing weight (kernel.py:236-237) and adds it into its own LDS
+// accumulator of (token, hidden row). Items come in expert order, so each token's
+// contributions are added in ascending local expert order, and the rows of one token inside
+// an item (a repeated expert id) in slot order; the work-group then sums its four K quarters
+// in fixed order and writes the 32 columns of every token, zeros for tokens without a local
+// expert (the zero-fill and finalize of kernel.py:704, 729). Deterministic, no atomics.
+// Slice width, measured at T=64 / T=16 (GEMM2 with the requantisation before it, us): one
+// fragment 78.0 / 39.8, two 63.9 / 33.7, four 101.6 / 52.6, against 68.0 / 40.0 for the
+// wavefront-per-unit GEMM2 plus combine_kernel. One fragment spends a 2 KB activation
+// fragment and four small loads on every 2 KB of weights; four need more registers than two
+// wavefronts per SIMD allow, and one wavefront per SIMD cannot keep the matrix core busy.
+constexpr int kSliceF = 2;                               // weight fragments per wavefront
+constexpr int kSliceQuarters = 4;                        // wavefronts per work-group = K quarters
+constexpr int kSliceSteps = kIBlocks / kSliceQuarters;   // 4 K-steps per quarter and item
+constexpr int kSliceRing = kSliceSteps;                  // ring slots: 3 steps in flight
+constexpr int kHiddenSlices = kHidden / (16 * kSliceF);  // 224
+static_assert(kSliceRing == kSliceSteps, "one ring turn per item: slot u is K-step u of the item");
+static_assert(kFusedItems <= 64, "one work item per lane");
+
+struct SliceStage {
+  v8i w[kSliceF];   // W2 fragments: the slice's hidden rows 16f.. x 128 K bytes
+  v8i a;            // act fragment: the item's 16 rows (rows past its end repeat its first row)
+  float sa;         // act scale of the lane's row for this K block
+  float sw;         // W2 block scale (the same for every lane)
+  int tok;          // token of the lane's row
+  float wt;         // routing weight of the lane's row
+};
+
+__global__ __launch_bounds__(kSliceQuarters * 64) void gemm2_slice_kernel(GemmParams p) {
+  __shared__ __attribute__((aligned(16))) float acc_lds[kSliceQuarters][kFusedDispatchTokens][16 * kSliceF];
+  const int lane = threadIdx.x & 63;
+  const int q = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int m = lane & 15;
+  const int T = p.T;
+  const int n_items = min(p.counters[kCtrItems], min(p.max_items, kFusedItems));
+  const int4 my_item = lane < n_items ? reinterpret_cast<const int4*>(p.work_items)[lane] : make_int4(0, 0, 0, 0);
+  const int nsteps = n_items * kSliceSteps;
+  const v4f zero = {0.f, 0.f, 0.f, 0.f};
+  for (int slice = blockIdx.x; slice < kHiddenSlices; slice += gridDim.x) {
+    const int h0 = slice * 16 * kSliceF;
+    float* my_acc = &acc_lds[q][0][0];
+    for (int i = lane; i < T * 16 * kSliceF; i += 64) my_acc[i] = 0.f;
+    if (nsteps > 0) {
+      // loads of flattened step st = 4 * item + j (K-step 4q + j of the item); steps past the
+      // last repeat it (cache-hot, never consumed)
+      auto issue = [&](int st, SliceStage& g) {
+        const int sc = min(st, nsteps - 1);
+        const int it = sc / kSliceSteps;
+        const int ks = q * kSliceSteps + (sc - it * kSliceSteps);
+        const int e = __builtin_amdgcn_readlane(my_item.x, it);
+        const int r0 = __builtin_amdgcn_readlane(my_item.y, it);
+        const int rows = __builtin_amdgcn_readlane(my_item.z, it);
+        const int r = r0 + (m < rows ? m : 0);
+#pragma unroll
+        for (int f = 0; f < kSliceF; ++f)
+          g.w[f] = load_frag(p.w2 + ((size_t)e * kHidden + h0 + 16 * f + m) * kInter + ks * 128 + (lane >> 4) * 16);
+        g.a = load_frag(p.act + (size_t)r * kInter + ks * 128 + (lane >> 4) * 16);
+        g.sa = p.act_scale[(size_t)r * kIBlocks + ks];
+        g.sw = p.w2_scale[((size_t)e * kHBlocks + h0 / 128) * kIBlocks + ks];
+        g.tok = p.sorted_token[r];
+        g.wt = p.sorted_weight[r];
+      };
+      SliceStage ring[kSliceRing];
+#pragma unroll
+      for (int u = 0; u < kSliceRing - 1; ++u) issue(u, ring[u]);
+      v4f acc[kSliceF];
+#pragma unroll
+      for (int f = 0; f < kSliceF; ++f) acc[f] = zero;
+#pragma nounroll
+      for (int st0 = 0; st0 < nsteps; st0 += kSliceSteps) {
+#pragma unroll
+        for (int u = 0; u < kSliceSteps; ++u) {
+          issue(st0 + u + kSliceRing - 1, ring[(u + kSliceRing - 1) % kSliceRing]);
+          __builtin_amdgcn_sched_barrier(0);
+          const SliceStage& g = ring[u];
+          const float sc = g.sa * g.sw;
+#pragma unroll
+          for (int f = 0; f < kSliceF; ++f) {
+            const v4f d = mfma16x16x128_fp8(g.w[f], g.a, zero);
+            acc[f] += d * sc;
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        // end of the item: its weighted rows into this wavefront's token accumulators; when a
+        // token names a local expert more than once its rows are adjacent (slot order), and
+        // the first one adds the others in order, so that each accumulator has one writer
+        const SliceStage& g = ring[kSliceSteps - 1];
+        const int rows = __builtin_amdgcn_readlane(my_item.z, st0 / kSliceSteps);
+        const bool live = m < rows;
+        const int prev = __shfl(g.tok, lane - 1);
+        const bool head = live && (m == 0 || prev != g.tok);
+        const bool dups = __ballot(live && !head) != 0;
+#pragma unroll
+        for (int f = 0; f < kSliceF; ++f) {
+          v4f v = acc[f] * g.wt;
+          acc[f] = zero;
+          if (dups) {
+            v4f tot = v;
+            bool run = true;
+            for (int d = 1; d < 16; ++d) {
+              const int ot = __shfl(g.tok, lane + d);
+              v4f ov;
+#pragma unroll
+              for (int i = 0; i < 4; ++i) ov[i] = __shfl(v[i], lane + d);
+              run = run && m + d < rows && ot == g.tok;
+              if (run) tot += ov;
+            }
+            v = tot;
+          }
+          if (head) *reinterpret_cast<v4f*>(&acc_lds[q][g.tok][16 * f + 4 * (lane >> 4)]) += v;
+        }
+      }
+    }
+    __syncthreads();
+    // the four K quarters, summed in fixed order: 4 columns of one token per thread
+    for (int i = threadIdx.x; i < T * 4 * kSliceF; i += kSliceQuarters * 64) {
+      const int t = i / (4 * kSliceF), c = 4 * (i % (4 * kSliceF));
+      const v4f s = ((*reinterpret_cast<const v4f*>(&acc_lds[0][t][c]) + *reinterpret_cast<const v4f*>(&acc_lds[1][t][c])) +
+                     *reinterpret_cast<const v4f*>(&acc_lds[2][t][c])) +
+                    *reinterpret_cast<const v4f*>(&acc_lds[3][t][c]);
+      const size_t o = (size_t)t * kHidden + h0 + c;
+      if (p.out_dtype == MOE_FP8_OUT_BF16)
+        *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(p.out) + o) = pack_bf16x4(s[0], s[1], s[2], s[3]);
+      else
+        *reinterpret_cast<v4f*>(reinterpret_cast<float*>(p.out) + o) = s;
+    }
+    __syncthreads();
+  }
+}
+
 // Output rows of every token without exactly one local assignment: the sum of its parked
 // GEMM2 rows in top-k slot order, or zeros. One wavefront per (token, 1/7 of the row): the
 // token's local slots become a uniform bit mask, and each lane sums 4 columns in 4 places.
@@ -542,11 +680,17 @@ hipError_t launch_requant(const GemmParams& p, int rows_per_item, hipStream_t s)
 
 hipError_t launch_gemm2(const GemmParams& p, int rows_per_item, hipStream_t s) {
   if (rows_per_item > 32) return launch_gemm2_tile(p, rows_per_item, s);
+  if (rows_per_item == kFusedItemRows) {
+    // up to 64 tokens: GEMM2 with the combine, one work-group per 32-row hidden slice
+    if (p.T > kFusedDispatchTokens) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(gemm2_slice_kernel, dim3(kHiddenSlices), dim3(kSliceQuarters * 64), 0, s, p);
+    return hipGetLastError();
+  }
   return launch_stream<kG2>(p, rows_per_item, s);
 }
 
-hipError_t launch_combine(const GemmParams& p, hipStream_t s) {
-  if (p.T <= 0) return hipSuccess;
+hipError_t launch_combine(const GemmParams& p, int rows_per_item, hipStream_t s) {
+  if (p.T <= 0 || rows_per_item == kFusedItemRows) return hipSuccess;   // combined in GEMM2
   int grid = (p.T * kCombineChunks + 3) / 4;   // 4 (token, chunk) items per work-group at a time
   if (grid > num_cus() * 8) grid = num_cus() * 8;
   hipLaunchKernelGGL(combine_kernel, dim3(grid), dim3(256), 0, s, p);

@@ -5,13 +5,15 @@
 //   workspace arrays : moe_fp8_layout offsets; every array is 256-byte aligned.
 // Kernels of one call run in this order on one stream:
 //   T <= 64 (moe_fp8_run): route_kernel<false> -> gemm1_stream_dispatch_kernel (GEMM1 that
-//   rebuilds the dispatch itself) -> requant_kernel -> GEMM2 -> combine_kernel; otherwise
+//   rebuilds the dispatch itself) -> requant_kernel -> gemm2_slice_kernel (GEMM2 and the
+//   combine); otherwise
 //   route_dispatch_small_kernel | (route_kernel<false> -> dispatch_small_kernel)
 //   | (route_kernel<true> -> scan_kernel -> place_kernel)
-//   -> GEMM1 -> [requant_kernel] -> GEMM2 -> combine_kernel
-// where, with <= 32 rows per work item, the GEMMs are gemm_stream_kernel<1|2> and GEMM1
-// leaves fp32 SwiGLU rows for requant_kernel; with more rows both are gemm_tile_kernel and
-// GEMM1 requantises in its epilogue.
+//   -> GEMM1 -> [requant_kernel] -> GEMM2 -> [combine_kernel]
+// where, with <= 32 rows per work item, GEMM1 is gemm_stream_kernel<1> and leaves fp32 SwiGLU
+// rows for requant_kernel, and GEMM2 is gemm2_slice_kernel (16-row items, up to 64 tokens)
+// or gemm_stream_kernel<2> followed by combine_kernel; with more rows both GEMMs are
+// gemm_tile_kernel, GEMM1 requantises in its epilogue and combine_kernel follows GEMM2.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -129,7 +131,7 @@ hipError_t launch_gemm1(const GemmParams& p, int rows_per_item, hipStream_t s);
 hipError_t launch_gemm1_dispatch(const GemmParams& p, const RouteParams& rp, hipStream_t s);
 hipError_t launch_requant(const GemmParams& p, int rows_per_item, hipStream_t s);
 hipError_t launch_gemm2(const GemmParams& p, int rows_per_item, hipStream_t s);
-hipError_t launch_combine(const GemmParams& p, hipStream_t s);
+hipError_t launch_combine(const GemmParams& p, int rows_per_item, hipStream_t s);
 hipError_t launch_gemm1_tile(const GemmParams& p, int rows_per_item, hipStream_t s);
 hipError_t launch_quantize_hidden(const void* x, int dtype, int T, uint8_t* q, float* scale, hipStream_t s);
 hipError_t launch_gemm2_tile(const GemmParams& p, int rows_per_item, hipStream_t s);

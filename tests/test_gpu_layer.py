@@ -281,8 +281,9 @@ def test_tile_stage_repeated(name):
     assert torch.equal(whole.view(torch.int16), out.view(torch.int16)), "staged and whole-layer runs differ"
 
 
-def test_deterministic_and_fp32_output():
-    kw, npkw = _workload("t1024_off64")
+@pytest.mark.parametrize("name", ["t64", "t1024_off64"])
+def test_deterministic_and_fp32_output(name):
+    kw, npkw = _workload(name)
     a = _run_full(kw)
     b = _run_full(kw)
     assert torch.equal(a.view(torch.int16), b.view(torch.int16)), "two runs differ bitwise"
