@@ -79,16 +79,17 @@ def routing_stats(ws, T):
 
 def workload_figures(T, n, e_touched, u, rows_per_item):
     """Algorithmic work of the layer and of its GEMM1 kernel. GEMM1 reads the touched experts'
-    W13 and block scales and each token's hidden row and scales once; in the decode regime
-    (items of <= 32 rows) it writes each assignment's fp32 SwiGLU row (8,192 B) and reads the
-    top-k lists (64 B per token, for the dispatch it rebuilds up to 64 tokens); on the tile path
-    it writes the requantised fp8 row and its 16 scales (2,112 B)."""
+    W13 and block scales and each token's hidden row and scales once. Per assignment it writes,
+    in the decode regime (items of <= 32 rows), the fp32 SwiGLU row (8,192 B), and up to 64
+    tokens it reads the top-k lists (64 B per token) for the dispatch it rebuilds; on the tile
+    path it writes the requantised fp8 row and its 16 scales (2,112 B)."""
     layer_bytes = e_touched * BYTES_PER_EXPERT + T * BYTES_PER_TOKEN + 512
     layer_flops = n * FLOPS_PER_ASSIGNMENT
+    g1_bytes = e_touched * G1_BYTES_PER_EXPERT + u * (7168 + 224)
     if rows_per_item <= 32:
-        g1_bytes = e_touched * G1_BYTES_PER_EXPERT + u * (7168 + 224) + n * 2048 * 4 + T * 64
+        g1_bytes += n * 2048 * 4 + (T * 64 if rows_per_item == 16 else 0)
     else:
-        g1_bytes = e_touched * G1_BYTES_PER_EXPERT + u * (7168 + 224) + n * (2048 + 64)
+        g1_bytes += n * (2048 + 16 * 4)
     return dict(layer_bytes=layer_bytes, layer_flops=layer_flops, g1_bytes=g1_bytes,
                 g1_flops=n * G1_FLOPS_PER_ASSIGNMENT, g2_flops=n * G2_FLOPS_PER_ASSIGNMENT)
 

@@ -110,15 +110,18 @@ typedef struct moe_fp8_args {
  *   counters      int32 [80]        [0] number of work items, [1] N; the rest internal
  *                                   (the tile kernels' work-list state)
  *   act           fp8   [N_max, 2048]    SwiGLU output requantised to e4m3fn          (kernel.py:669)
- *   act_scale     fp32  [N_max, 16]      its 1x128 block scales, row-major per row   (kernel.py:670)
- *                 Deliberate difference: the reference requantises per 1x64 block (BLOCK_N_1 = 64,
- *                 kernel.py:131-135, :643, scales [32, N]); this layer per 1x128, so that GEMM2
- *                 applies one activation scale per 128-wide K block, like every other operand.
- *                 The parity tests bound the output's distance from fp32 math by that of the
- *                 64-column algorithm (per token at most 2x its maximum error + 1/64).
+ *   act_scale     fp32  [N_max, 2048/requant_block]  its 1 x requant_block scales, row-major
+ *                                        per row                                      (kernel.py:670)
+ *                 requant_block is 64 up to 64 tokens, the reference's 1x64 block (BLOCK_N_1 = 64,
+ *                 kernel.py:131-135, :643, scales [32, N]). Above 64 tokens it is 128, a
+ *                 deliberate difference: GEMM2 then applies one activation scale per 128-wide K
+ *                 block, like every other operand. The parity tests bound the output's distance
+ *                 from fp32 math by that of the 64-column algorithm (per token at most 2x its
+ *                 maximum error + 1/64).
  *   partial       fp32  [T*8, 7168]      weighted GEMM2 rows of tokens with more than one local
- *                                        assignment, indexed by flat slot, above 64 tokens (up to
- *                                        64 the combine happens inside GEMM2)         (kernel.py:704)
+ *                                        assignment, indexed by flat slot, above 64 tokens (0
+ *                                        bytes up to 64: the combine happens inside GEMM2)
+ *                                                                                     (kernel.py:704)
  *   swiglu        fp32  [N_max, 2048]    SwiGLU output before requantisation; only for
  *                                        T <= 512 (0 bytes otherwise)
  */
@@ -145,7 +148,8 @@ typedef struct moe_fp8_layout {
   int32_t max_work_items;
   int32_t route_blocks;      /* routing work-groups */
   int32_t rows_per_item;     /* GEMM rows (assignments) per work item */
-  int32_t reserved[3];
+  int32_t requant_block;     /* columns per act_scale entry: 64 up to 64 tokens, else 128 */
+  int32_t reserved[2];
 } moe_fp8_layout;
 
 /* Workspace size for num_tokens tokens (0 if num_tokens is invalid). */
@@ -184,7 +188,7 @@ int moe_fp8_run_profiled(const moe_fp8_args* args, void* workspace, size_t works
  * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). No
  * counterpart in the reference, whose temporaries come from torch's allocator
  * (kernel.py:348-370, 629-630, 669-670, 704). The workspace is a device array inside the
- * library of MOE_FP8_STATIC_SCRATCH_BYTES (20 MiB), one per GPU that loads the library, held
+ * library of MOE_FP8_STATIC_SCRATCH_BYTES (6 MiB), one per GPU that loads the library, held
  * until the process ends; it holds the workspace of up to MOE_FP8_STATIC_MAX_TOKENS (64)
  * tokens, and larger batches return MOE_FP8_ESTATIC_TOKENS without launching anything.
  * Nothing is allocated or freed by this call (the first call on a device resolves the
@@ -193,7 +197,7 @@ int moe_fp8_run_profiled(const moe_fp8_args* args, void* workspace, size_t works
  * different threads without ordering) race and give wrong results; calls ordered on one
  * stream are safe, each rewriting what it reads. Results are bit-identical to moe_fp8_run. */
 #define MOE_FP8_STATIC_MAX_TOKENS    64
-#define MOE_FP8_STATIC_SCRATCH_BYTES (20u << 20)
+#define MOE_FP8_STATIC_SCRATCH_BYTES (6u << 20)
 int moe_fp8_run_static(const moe_fp8_args* args, hipStream_t stream);
 
 /* Stage 1: routing and dispatch. Writes topk_ids/topk_weights, the expert histogram,

@@ -41,7 +41,7 @@ EDEVICE = -7
 EINVAL_HIDDEN_DTYPE = -8
 ESTATIC_TOKENS = -9
 STATIC_MAX_TOKENS = 64
-STATIC_SCRATCH_BYTES = 20 << 20
+STATIC_SCRATCH_BYTES = 6 << 20
 
 EXPORTED_SYMBOLS = (
     "moe_fp8_workspace_bytes",
@@ -106,7 +106,8 @@ class MoeFp8Layout(ctypes.Structure):
         ("max_work_items", ctypes.c_int32),
         ("route_blocks", ctypes.c_int32),
         ("rows_per_item", ctypes.c_int32),
-        ("reserved", ctypes.c_int32 * 3),
+        ("requant_block", ctypes.c_int32),
+        ("reserved", ctypes.c_int32 * 2),
     ]
 
 

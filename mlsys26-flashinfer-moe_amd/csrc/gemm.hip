@@ -81,13 +81,16 @@ struct StreamStage {
   float sa[NG];
 };
 
-// One work unit for an item of NG row groups (NG <= 2). Every K-step has the same shape:
-// loads past the last step repeat the last step (cache-hot) into ring slots that are never
-// read, and the weight block scales come from lane registers through readlane, so the loop
-// holds no branches and the compiler's waits cover exactly the step being consumed.
+// The accumulators of one work unit for an item of NG row groups (NG <= 2). Every K-step
+// has the same shape: loads past the last step repeat the last step (cache-hot) into ring
+// slots that are never read, and the weight block scales come from lane registers through
+// readlane, so the loop holds no branches and the compiler's waits cover exactly the step
+// being consumed. Lane l ends with rows 4*(l/16)+i of each weight fragment against row
+// l%16 of each row group.
 template <int KIND, int NG>
-__device__ __forceinline__ void stream_unit(const GemmParams& p, int e, int r0, int rows, int slice, int lane,
-                                            const int32_t* row_token) {
+__device__ __forceinline__ void stream_accumulate(const GemmParams& p, int e, int r0, int rows, int slice,
+                                                  int lane, const int32_t* row_token,
+                                                  v4f (&acc)[StreamShape<KIND>::kFrags][NG]) {
   using S = StreamShape<KIND>;
   constexpr int KS = S::kSteps;
   constexpr int NF = S::kFrags;
@@ -156,7 +159,6 @@ __device__ __forceinline__ void stream_unit(const GemmParams& p, int e, int r0, 
 #pragma unroll
   for (int s = 0; s < NB - 1; ++s) issue_a(s, ring[s]);
 
-  v4f acc[NF][NG];
 #pragma unroll
   for (int f = 0; f < NF; ++f)
 #pragma unroll
@@ -188,7 +190,24 @@ __device__ __forceinline__ void stream_unit(const GemmParams& p, int e, int r0, 
   }
 #pragma unroll
   for (int u = 0; u < KS - KMAIN; ++u) step(KMAIN + u, u);
+}
 
+// SwiGLU of a GEMM1 unit's accumulators for row group g: silu(X2) * X1 (kernel.py:126-129).
+__device__ __forceinline__ v4f swiglu4(const v4f& x1, const v4f& x2) {
+  v4f c;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) c[i] = (x2[i] / (1.0f + __expf(-x2[i]))) * x1[i];
+  return c;
+}
+
+// One work unit with its epilogue: GEMM1 writes fp32 SwiGLU rows for requant_kernel; GEMM2
+// writes or parks the weighted rows.
+template <int KIND, int NG>
+__device__ __forceinline__ void stream_unit(const GemmParams& p, int e, int r0, int rows, int slice, int lane,
+                                            const int32_t* row_token) {
+  constexpr int NF = StreamShape<KIND>::kFrags;
+  v4f acc[NF][NG];
+  stream_accumulate<KIND, NG>(p, e, r0, rows, slice, lane, row_token, acc);
   // lane: column (lane & 15) of each row group, fragment rows 4*(lane>>4) + i
 #pragma unroll
   for (int g = 0; g < NG; ++g) {
@@ -196,13 +215,8 @@ __device__ __forceinline__ void stream_unit(const GemmParams& p, int e, int r0, 
     if (m >= rows) continue;
     const int pr = r0 + m;
     if constexpr (KIND == kG1) {
-      v4f c;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float x1 = acc[0][g][i], x2 = acc[1][g][i];
-        c[i] = (x2 / (1.0f + __expf(-x2))) * x1;
-      }
-      *reinterpret_cast<v4f*>(p.swiglu + (size_t)pr * kInter + slice * 16 + 4 * (lane >> 4)) = c;
+      *reinterpret_cast<v4f*>(p.swiglu + (size_t)pr * kInter + slice * 16 + 4 * (lane >> 4)) =
+          swiglu4(acc[0][g], acc[1][g]);
     } else {
       const int t = p.sorted_token[pr];
       const float wt = p.sorted_weight[pr];
@@ -254,6 +268,11 @@ __global__ __launch_bounds__(kStreamWaves * 64) void gemm_stream_kernel(GemmPara
   const int n_items = min(p.counters[kCtrItems], p.max_items);
   stream_units<KIND, MAXNG>(p, n_items, reinterpret_cast<const int4*>(p.work_items), p.sorted_token);
 }
+
+// Columns per requantisation scale of 16-row items: the reference's 1x64 block
+// (kernel.py:131-135); GEMM2 then applies two activation scales per 128-wide K block.
+constexpr int kQuantCols = 64;
+constexpr int kQuantBlocks = kInter / kQuantCols;    // 32 per row
 
 // Decode batches of up to kFusedDispatchTokens tokens: GEMM1 without a dispatch launch before
 // it. Every work-group rebuilds the call's dispatch from the top-k lists in LDS, the same as
@@ -378,10 +397,13 @@ __global__ __launch_bounds__(kStreamWaves * 64) void gemm1_stream_dispatch_kerne
   stream_units<kG1, 1>(p, s.n_items, s.items, s.row_token);
 }
 
-// Requantises the fp32 SwiGLU rows: per row and 128 columns, scale = max(amax/448, 1e-12)
-// and q = e4m3(c / scale) (kernel.py:131-135 with 128-column blocks). One work-group of 256
-// threads per row; 16 threads (8 columns each) per block.
+// Requantises the fp32 SwiGLU rows: per row and COLS columns, scale = max(amax/448, 1e-12)
+// and q = e4m3(c / scale) (kernel.py:131-135, whose blocks are 64 columns wide). One
+// work-group of 256 threads per row, 8 columns per thread, COLS/8 threads per block.
+template <int COLS>
 __global__ __launch_bounds__(256) void requant_kernel(GemmParams p) {
+  constexpr int kThreads = COLS / 8;
+  constexpr int kBlocks = kInter / COLS;
   const int nmax = p.T * kTopK;   // rows of the SwiGLU buffer
   const int tid = threadIdx.x;
   for (int r = blockIdx.x; r < nmax; r += gridDim.x) {
@@ -392,13 +414,13 @@ __global__ __launch_bounds__(256) void requant_kernel(GemmParams p) {
     float amax = fmaxf(fmaxf(fmaxf(fabsf(a[0]), fabsf(a[1])), fmaxf(fabsf(a[2]), fabsf(a[3]))),
                        fmaxf(fmaxf(fabsf(b[0]), fabsf(b[1])), fmaxf(fabsf(b[2]), fabsf(b[3]))));
 #pragma unroll
-    for (int off = 1; off < 16; off <<= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+    for (int off = 1; off < kThreads; off <<= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
     const float scale = fmaxf(amax / 448.0f, 1e-12f);
     uint2 q;
     q.x = pack_fp8x4(a[0] / scale, a[1] / scale, a[2] / scale, a[3] / scale);
     q.y = pack_fp8x4(b[0] / scale, b[1] / scale, b[2] / scale, b[3] / scale);
     reinterpret_cast<uint2*>(p.act + (size_t)r * kInter)[tid] = q;
-    if ((tid & 15) == 0) p.act_scale[(size_t)r * kIBlocks + (tid >> 4)] = scale;
+    if (tid % kThreads == 0) p.act_scale[(size_t)r * kBlocks + tid / kThreads] = scale;
   }
 }
 
@@ -429,7 +451,7 @@ static_assert(kFusedItems <= 64, "one work item per lane");
 struct SliceStage {
   v8i w[kSliceF];   // W2 fragments: the slice's hidden rows 16f.. x 128 K bytes
   v8i a;            // act fragment: the item's 16 rows (rows past its end repeat its first row)
-  float sa;         // act scale of the lane's row for this K block
+  float2 sa;        // act scales of the lane's row for the two 64-column halves of the K block
   float sw;         // W2 block scale (the same for every lane)
   int tok;          // token of the lane's row
   float wt;         // routing weight of the lane's row
@@ -464,7 +486,7 @@ __global__ __launch_bounds__(kSliceQuarters * 64) void gemm2_slice_kernel(GemmPa
         for (int f = 0; f < kSliceF; ++f)
           g.w[f] = load_frag(p.w2 + ((size_t)e * kHidden + h0 + 16 * f + m) * kInter + ks * 128 + (lane >> 4) * 16);
         g.a = load_frag(p.act + (size_t)r * kInter + ks * 128 + (lane >> 4) * 16);
-        g.sa = p.act_scale[(size_t)r * kIBlocks + ks];
+        g.sa = *reinterpret_cast<const float2*>(p.act_scale + (size_t)r * kQuantBlocks + 2 * ks);
         g.sw = p.w2_scale[((size_t)e * kHBlocks + h0 / 128) * kIBlocks + ks];
         g.tok = p.sorted_token[r];
         g.wt = p.sorted_weight[r];
@@ -482,11 +504,19 @@ __global__ __launch_bounds__(kSliceQuarters * 64) void gemm2_slice_kernel(GemmPa
           issue(st0 + u + kSliceRing - 1, ring[(u + kSliceRing - 1) % kSliceRing]);
           __builtin_amdgcn_sched_barrier(0);
           const SliceStage& g = ring[u];
-          const float sc = g.sa * g.sw;
+          // the act fragment's two 64-column halves carry their own scales: one MFMA per
+          // half, the other half's bytes zeroed (lanes hold bytes [16j, 16j+16) of the first
+          // half in a[0..3] and of the second in a[4..7])
+          const v4i kZero4 = {0, 0, 0, 0};
+          const v8i a_lo = join(lo_half(g.a), kZero4);
+          const v8i a_hi = join(kZero4, hi_half(g.a));
+          const float sc_lo = g.sa.x * g.sw, sc_hi = g.sa.y * g.sw;
 #pragma unroll
           for (int f = 0; f < kSliceF; ++f) {
-            const v4f d = mfma16x16x128_fp8(g.w[f], g.a, zero);
-            acc[f] += d * sc;
+            const v4f d_lo = mfma16x16x128_fp8(g.w[f], a_lo, zero);
+            const v4f d_hi = mfma16x16x128_fp8(g.w[f], a_hi, zero);
+            acc[f] += d_lo * sc_lo;
+            acc[f] += d_hi * sc_hi;
           }
           __builtin_amdgcn_sched_barrier(0);
         }
@@ -674,7 +704,11 @@ hipError_t launch_requant(const GemmParams& p, int rows_per_item, hipStream_t s)
   if (rows_per_item > 32) return hipSuccess;   // the tile GEMM1 requantises in its epilogue
   int grid = p.T * kTopK;                      // rows of the SwiGLU buffer
   if (grid > num_cus() * 8) grid = num_cus() * 8;
-  if (grid > 0) hipLaunchKernelGGL(requant_kernel, dim3(grid), dim3(256), 0, s, p);
+  if (grid <= 0) return hipSuccess;
+  if (requant_block_for(rows_per_item) == kQuantCols)
+    hipLaunchKernelGGL(requant_kernel<kQuantCols>, dim3(grid), dim3(256), 0, s, p);
+  else
+    hipLaunchKernelGGL(requant_kernel<128>, dim3(grid), dim3(256), 0, s, p);
   return hipGetLastError();
 }
 

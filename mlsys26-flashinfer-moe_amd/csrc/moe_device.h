@@ -74,6 +74,18 @@ __device__ __forceinline__ v8i join(const v4i& lo, const v4i& hi) {
   return r;
 }
 
+__device__ __forceinline__ v4i lo_half(const v8i& v) {
+  v4i r;
+  r[0] = v[0]; r[1] = v[1]; r[2] = v[2]; r[3] = v[3];
+  return r;
+}
+
+__device__ __forceinline__ v4i hi_half(const v8i& v) {
+  v4i r;
+  r[0] = v[4]; r[1] = v[5]; r[2] = v[6]; r[3] = v[7];
+  return r;
+}
+
 __device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & 63); }
 
 __device__ __forceinline__ uint64_t lanemask_lt() {

@@ -9,12 +9,13 @@ mode="definition": the intermediate C stays fp32 (the definition's math); each t
   output sums its experts' weighted rows in ascending expert order, as the definition's
   loop over experts does.
 mode="emulated":   C is requantised to e4m3 with one scale per row per `requant_block`
-  columns before GEMM2 (kernel.py:131-135 uses 64; the HIP kernels use 128), and each
-  token sums its weighted rows in top-k slot order starting from 0, as the HIP combine
-  does; a token with one local assignment gets exactly that row. With `act_override`
-  = (act uint8 [N, I], act_scale fp32 [N, I/128]) in bucket-row order, GEMM1 is skipped
-  and GEMM2 + combine run on that intermediate instead of the oracle's own: a check of
-  the second half of the layer on exactly the intermediate a kernel produced.
+  columns before GEMM2 (kernel.py:131-135 uses 64; the HIP kernels use 64 up to 64 tokens
+  and 128 above), and each token sums its weighted rows in top-k slot order starting from
+  0, as the HIP combine does; a token with one local assignment gets exactly that row.
+  With `act_override` = (act uint8 [N, I], act_scale fp32 [N, I/requant_block]) in
+  bucket-row order, GEMM1 is skipped and GEMM2 + combine run on that intermediate instead
+  of the oracle's own: a check of the second half of the layer on exactly the
+  intermediate a kernel produced.
 Weights are dequantised one touched expert at a time (kept in `dequant_cache`, a dict the
 caller owns, when given, so that several calls on one weight set dequantise each expert
 once); `tokens` restricts the GEMMs and the output to a subset of tokens (routing still
@@ -54,8 +55,8 @@ def layer_forward(routing_logits, routing_bias, hidden_states, hidden_states_sca
     (all tokens when None)."""
     if mode not in ("definition", "emulated"):
         raise ValueError(mode)
-    if act_override is not None and (mode != "emulated" or requant_block != 128):
-        raise ValueError("act_override needs mode='emulated' with 128-column blocks")
+    if act_override is not None and mode != "emulated":
+        raise ValueError("act_override needs mode='emulated'")
     hidden = np.asarray(hidden_states, dtype=np.uint8)
     T, H = hidden.shape
     e_local, two_i, _ = gemm1_weights.shape

@@ -49,13 +49,18 @@ def test_layout_consistent(pkg, T):
     assert L.route_blocks == (T + 15) // 16
     assert L.max_work_items == 32 + (8 * T + L.rows_per_item - 1) // L.rows_per_item
     assert L.counters == 0
+    # up to 64 tokens (16-row items) the requantisation is per 64 columns and GEMM2 combines in
+    # LDS (no parked rows); items of up to 32 rows keep GEMM1's fp32 SwiGLU rows
+    decode = L.rows_per_item == 16
+    assert L.rows_per_item == (16 if T <= 64 else 32 if T <= 512 else L.rows_per_item)
+    assert L.requant_block == (64 if decode else 128)
     arrays = [
         ("topk_ids", 4 * 8 * T), ("topk_weights", 4 * 8 * T), ("expert_count", 4 * 32),
         ("expert_start", 4 * 33), ("sorted_token", 4 * 8 * T), ("sorted_weight", 4 * 8 * T),
         ("sorted_slot", 4 * 8 * T), ("token_nlocal", 4 * T), ("slot_rank", 4 * 8 * T),
         ("block_count", 4 * 32 * L.route_blocks), ("work_items", 16 * L.max_work_items),
-        ("counters", 4 * 80), ("act", 8 * T * 2048), ("act_scale", 4 * 8 * T * 16),
-        ("partial", 4 * 8 * T * 7168),
+        ("counters", 4 * 80), ("act", 8 * T * 2048), ("act_scale", 4 * 8 * T * 2048 // L.requant_block),
+        ("partial", 0 if decode else 4 * 8 * T * 7168),
         ("swiglu", 4 * 8 * T * 2048 if L.rows_per_item <= 32 else 0),
     ]
     spans = sorted((getattr(L, n), getattr(L, n) + b, n) for n, b in arrays)

@@ -2,7 +2,8 @@
 
 The layer is checked in two halves and as a whole, on bf16 output compared as float32:
   * GEMM1 + SwiGLU + requantisation, through the fp8 intermediate it leaves in the
-    workspace, against the emulated oracle (the kernels' algorithm: 1x128 requantisation):
+    workspace, against the emulated oracle (the kernels' algorithm: 1x64 requantisation up
+    to 64 tokens, as the reference's, and 1x128 above; the layout reports which):
     scales within 3e-4 relative, at most 1% of the bytes different, each by at most one
     fp8 step (plus 4e-4 of the row maximum for the MFMA's block-sum precision).
   * GEMM2 + weighted combine, on exactly that intermediate (the oracle's act_override):
@@ -15,7 +16,8 @@ The layer is checked in two halves and as a whole, on bf16 output compared as fl
     every element of the token's output row moves by a few hundredths.)
   * The whole layer against the definition (fp32 intermediate, kernel.py's math without
     requantisation): relative RMS <= 0.05; and against the reference's own algorithm, which
-    requantises per 64 columns (kernel.py:131-135) where these kernels use 128, per token
+    requantises per 64 columns (kernel.py:131-135) where these kernels use 128 above 64
+    tokens (below, the same algorithm in another summation order), per token
         max_j |gpu - def| <= 2 * max_j |ref64 - def| + 1/64,
     and over all checked elements rms(gpu - def) <= 1.25 * rms(ref64 - def). The factor 2:
     on the CPU the 128-column algorithm's per-token maximum reaches 1.56x the 64-column
@@ -89,10 +91,18 @@ def _run_full(kw, out_dtype=torch.bfloat16):
     return out
 
 
+def _requant_block(T):
+    """Columns per activation scale of the layer at T tokens, from the library's layout."""
+    rb = int(_gh()._lib.workspace_layout(T).requant_block)
+    assert rb == (64 if T <= 64 else 128)
+    return rb
+
+
 def _read_act(ws, n):
     gh = _gh()
+    nb = 2048 // int(ws.layout.requant_block)
     act = gh.read(ws, "act", torch.uint8, n * 2048).reshape(n, 2048)
-    sc = gh.read(ws, "act_scale", torch.float32, n * 16).reshape(n, 16)
+    sc = gh.read(ws, "act_scale", torch.float32, n * nb).reshape(n, nb)
     return act, sc
 
 
@@ -107,9 +117,10 @@ def _check_intermediate(act, sc, emu, rows, what):
     assert np.mean(diff) <= 0.01
     # Dequantised, the two intermediates differ by at most one fp8 step (12.5% of the
     # value) plus the accumulation difference, which is absolute: 4e-4 of the row maximum.
-    deq_g = ofp8.decode(a) * np.repeat(s, 128, axis=1)
-    deq_r = ofp8.decode(ra) * np.repeat(rs, 128, axis=1)
-    row_max = 448.0 * np.repeat(rs, 128, axis=1)
+    rb = 2048 // s.shape[1]
+    deq_g = ofp8.decode(a) * np.repeat(s, rb, axis=1)
+    deq_r = ofp8.decode(ra) * np.repeat(rs, rb, axis=1)
+    row_max = 448.0 * np.repeat(rs, rb, axis=1)
     err = np.abs(deq_g - deq_r)
     bound = 0.125 * np.abs(deq_r) + 4e-4 * row_max
     print(f"{what}: intermediate max err / bound {np.max(err / bound, initial=0):.3f}", flush=True)
@@ -118,7 +129,8 @@ def _check_intermediate(act, sc, emu, rows, what):
 
 def _check_second_half(got, npkw, act, sc, tokens, what, topk=None):
     """GEMM2 + combine on the GPU's own intermediate: one bf16 step + block-sum precision."""
-    ref = olayer.layer_forward(**npkw, mode="emulated", tokens=tokens, topk=topk, act_override=(act, sc))["output"]
+    ref = olayer.layer_forward(**npkw, mode="emulated", tokens=tokens, topk=topk, act_override=(act, sc),
+                               requant_block=2048 // sc.shape[1])["output"]
     row_max = np.max(np.abs(ref), axis=1, keepdims=True)
     err = np.abs(got - ref)
     bound = 2.0 ** -7 * np.abs(ref) + 4e-4 * row_max
@@ -138,8 +150,8 @@ def _wanted_rows(emu, tokens):
 @pytest.mark.parametrize("name,sample", [("t16", None), ("t64", None), ("t256", None), ("t1024_off64", None),
                                          ("t8192", 256), ("t4096_skew", 256), ("t32768", 24)])
 def test_layer_matches_oracle(name, sample):
+    gh = _gh()   # registers the package
     from mlsys26_flashinfer_moe_amd import moe
-    gh = _gh()
     kw, npkw = _workload(name)
     T = kw["routing_logits"].shape[0]
     print(f"layer {name} T={T}", flush=True)
@@ -152,7 +164,7 @@ def test_layer_matches_oracle(name, sample):
         tokens = np.sort(rng.choice(T, sample, replace=False))
     sel = slice(None) if tokens is None else tokens
     g = got[sel]
-    emu = olayer.layer_forward(**npkw, mode="emulated", tokens=tokens)
+    emu = olayer.layer_forward(**npkw, mode="emulated", tokens=tokens, requant_block=_requant_block(T))
     n = len(emu["sorted_slot"])
     ws = moe.workspace_for(T, kw["routing_logits"].device)   # the workspace run() used
     assert gh.counters(ws)[1] == n
@@ -237,7 +249,7 @@ def test_intermediate_fp8_matches_oracle(name):
     args = gh.make_args(**kw, output=out)
     gh.route_dispatch(args, ws)
     gh.gemm1(args, ws)
-    emu = olayer.layer_forward(**npkw, mode="emulated")
+    emu = olayer.layer_forward(**npkw, mode="emulated", requant_block=_requant_block(T))
     n = len(emu["sorted_slot"])
     assert gh.counters(ws)[1] == n
     if ws.layout.rows_per_item <= 32:
@@ -363,7 +375,7 @@ def test_layer_edge_cases_given_topk(T, case):
     tokens = None if T <= 40 else np.sort(rng.choice(T, 24, replace=False))
     if case == "few_local":   # every kind of token: 2 local experts, each item's edges, none
         tokens = np.unique(np.concatenate([tokens, [0, 39, 40, 299, 300, 459, 460, 479, 480, 639, 640, T - 1]]))
-    emu = olayer.layer_forward(**npkw, mode="emulated", topk=(ids, tw), tokens=tokens)
+    emu = olayer.layer_forward(**npkw, mode="emulated", topk=(ids, tw), tokens=tokens, requant_block=_requant_block(T))
     sel = slice(None) if tokens is None else tokens
     if case == "none_local":
         assert np.all(got == 0)
@@ -397,7 +409,7 @@ def test_layer_last_expert_group():
     npkw = gh.to_numpy_inputs({**kw, "gemm1_weights": w[0][:1], "gemm2_weights": w[2][:1]})
     npkw["gemm1_weights"], npkw["gemm1_weights_scale"], npkw["gemm2_weights"], npkw["gemm2_weights_scale"] = wnp
     npkw["dequant_cache"] = _WEIGHTS["cache"]
-    emu = olayer.layer_forward(**npkw, mode="emulated")
+    emu = olayer.layer_forward(**npkw, mode="emulated", requant_block=_requant_block(T))
     assert emu["token_nlocal"].sum() > 0
     from mlsys26_flashinfer_moe_amd import moe
     n = len(emu["sorted_slot"])

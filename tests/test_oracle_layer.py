@@ -111,19 +111,29 @@ def test_dequant_cache_gives_the_same_result():
     assert len(cache) > 0
 
 
-def test_act_override_reproduces_emulated_mode():
+@pytest.mark.parametrize("requant_block", [64, 128])
+def test_act_override_reproduces_emulated_mode(requant_block):
     """GEMM2 + combine on a given intermediate: fed the emulated mode's own fp8 intermediate,
-    the result is bit-identical; a changed intermediate byte changes the output of (only) the
-    tokens whose rows use it."""
+    the result is bit-identical; a changed intermediate byte, or a changed scale of the row's
+    last block, changes the output of (only) the tokens whose rows use it."""
     kw, topk = _inputs(5, 5)
-    ref = olayer.layer_forward(**kw, mode="emulated", topk=topk)
+    ref = olayer.layer_forward(**kw, mode="emulated", topk=topk, requant_block=requant_block)
     act, sc = ref["act"].copy(), ref["act_scale"].copy()
-    got = olayer.layer_forward(**kw, mode="emulated", topk=topk, act_override=(act, sc))
+    assert sc.shape[1] == kw["gemm2_weights"].shape[2] // requant_block
+    got = olayer.layer_forward(**kw, mode="emulated", topk=topk, act_override=(act, sc),
+                               requant_block=requant_block)
     assert np.array_equal(got["output_f32"], ref["output_f32"])
     row = 0
     tok = int(ref["sorted_token"][row])
     act[row, 3] ^= 0x01                          # one code step
-    moved = olayer.layer_forward(**kw, mode="emulated", topk=topk, act_override=(act, sc))
+    moved = olayer.layer_forward(**kw, mode="emulated", topk=topk, act_override=(act, sc),
+                                 requant_block=requant_block)
+    diff = np.any(moved["output_f32"] != ref["output_f32"], axis=1)
+    assert diff[tok] and diff.sum() == 1
+    act[row, 3] ^= 0x01
+    sc[row, -1] *= 2.0                           # the row's last requant_block columns
+    moved = olayer.layer_forward(**kw, mode="emulated", topk=topk, act_override=(act, sc),
+                                 requant_block=requant_block)
     diff = np.any(moved["output_f32"] != ref["output_f32"], axis=1)
     assert diff[tok] and diff.sum() == 1
     with pytest.raises(ValueError):
