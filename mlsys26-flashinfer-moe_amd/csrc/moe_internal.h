@@ -99,7 +99,7 @@ struct RouteParams {
   int32_t* sorted_slot;
   int32_t* token_nlocal;
   int32_t* slot_rank;
-  int32_t* block_count;  // [nblocks, 32], becomes the exclusive prefix over blocks
+  int32_t* block_count;  // [nblocks, 32] expert histogram of each routing work-group
   int32_t* work_items;   // [max_items, 4]
   int32_t* counters;
 };

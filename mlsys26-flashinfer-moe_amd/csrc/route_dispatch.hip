@@ -8,8 +8,9 @@
 //             in LDS (one launch);
 //   T <= 256 (or given top-k lists): route_kernel<false> (16 tokens per work-group) ->
 //             dispatch_small_kernel, which does the whole dispatch in one work-group, in LDS;
-//   larger T: route_kernel<true> (also per work-group histograms and ranks) -> scan_kernel
-//             -> place_kernel. No kernel synchronises across work-groups.
+//   larger T: route_kernel<true> (also per work-group histograms and ranks) -> place_kernel
+//             (each work-group reduces the histograms it needs). No kernel synchronises
+//             across work-groups.
 //
 // The order inside an expert's bucket is ascending token (then slot), i.e. a stable sort
 // by expert of the flat top-k list; the reference's atomic scatter (kernel.py:288-324)
@@ -454,65 +455,76 @@ __global__ __launch_bounds__(kRouteThreads) void dispatch_small_kernel(RoutePara
   }
 }
 
-// Large batches, step 2 (one work-group): per-expert exclusive prefix of the work-group
-// histograms (in place), CSR offsets and the work list. Thread (j, e) owns a run of the
-// work-groups for expert e; it reads their counts kScanBatch at a time, all loads of a batch
-// in flight together (a load-then-add loop would wait out one memory latency per count).
+// Large batches, step 2: each local slot to its bucket position. Every work-group reduces the
+// routing work-groups' histograms itself (no scan launch in between): thread (j, e) sums the
+// counts of expert e over the blocks b = j mod kPlaceGroups, both over the blocks before its
+// own (its exclusive prefix) and over all of them (the expert's total), kScanBatch loads in
+// flight at a time; the partial sums meet in LDS. Work-group 0 also writes the CSR offsets,
+// the counters and the work list (finish_counts); every work-group derives the same offsets.
 constexpr int kScanBatch = 16;
+constexpr int kPlaceThreads = 512;
+constexpr int kPlaceGroups = kPlaceThreads / kExpertsLocal;   // 16
+static_assert(kRouteTokensPerBlock * kTopK <= kPlaceThreads, "one slot per thread");
 
-__global__ __launch_bounds__(kRouteThreads) void scan_kernel(RouteParams p) {
-  __shared__ int s_part[32][kExpertsLocal];
+__global__ __launch_bounds__(kPlaceThreads) void place_kernel(RouteParams p) {
+  __shared__ int s_pre[kPlaceGroups][kExpertsLocal];
+  __shared__ int s_tot[kPlaceGroups][kExpertsLocal];
+  __shared__ int s_prefix[kExpertsLocal];
   __shared__ int s_start[kExpertsLocal + 1];
   const int tid = threadIdx.x;
+  const int b = blockIdx.x;
   const int nb = p.nblocks;
-  const int e = tid & 31, j = tid >> 5;   // 32 threads per expert
-  const int chunk = (nb + 31) / 32;
-  const int b0 = min(nb, j * chunk), b1 = min(nb, b0 + chunk);
-  int sum = 0;
-  for (int bb = b0; bb < b1; bb += kScanBatch) {
+  // this thread's slot, loaded before the reduction so that the loads overlap it
+  const int s = b * kRouteTokensPerBlock * kTopK + tid;
+  const bool has_slot = tid < kRouteTokensPerBlock * kTopK && s < p.T * kTopK;
+  const int le = has_slot ? local_of(p.topk_ids[s], p.offset) : -1;
+  const int rank = le >= 0 ? p.slot_rank[s] : 0;
+  const float w = le >= 0 ? p.topk_w[s] : 0.f;
+
+  const int e = tid % kExpertsLocal, j = tid / kExpertsLocal;
+  int pre = 0, tot = 0;
+  for (int b0 = j; b0 < nb; b0 += kPlaceGroups * kScanBatch) {
     int v[kScanBatch];
-#pragma unroll
-    for (int i = 0; i < kScanBatch; ++i) v[i] = bb + i < b1 ? p.block_count[(bb + i) * kExpertsLocal + e] : 0;
-#pragma unroll
-    for (int i = 0; i < kScanBatch; ++i) sum += v[i];
-  }
-  s_part[j][e] = sum;
-  __syncthreads();
-  if (tid < kExpertsLocal) {
-    int run = 0;
-    for (int jj = 0; jj < 32; ++jj) {
-      const int v = s_part[jj][tid];
-      s_part[jj][tid] = run;
-      run += v;
-    }
-    finish_counts(p, tid, run, s_start);
-  }
-  __syncthreads();
-  int run = s_part[j][e];
-  for (int bb = b0; bb < b1; bb += kScanBatch) {
-    int v[kScanBatch];
-#pragma unroll
-    for (int i = 0; i < kScanBatch; ++i) v[i] = bb + i < b1 ? p.block_count[(bb + i) * kExpertsLocal + e] : 0;
 #pragma unroll
     for (int i = 0; i < kScanBatch; ++i) {
-      if (bb + i < b1) p.block_count[(bb + i) * kExpertsLocal + e] = run;
-      run += v[i];
+      const int bb = b0 + i * kPlaceGroups;
+      v[i] = bb < nb ? p.block_count[bb * kExpertsLocal + e] : 0;
+    }
+#pragma unroll
+    for (int i = 0; i < kScanBatch; ++i) {
+      tot += v[i];
+      pre += (b0 + i * kPlaceGroups < b) ? v[i] : 0;
     }
   }
-}
-
-// Large batches, step 3: each local slot to its bucket position.
-__global__ __launch_bounds__(kRouteTokensPerBlock * kTopK) void place_kernel(RouteParams p) {
-  __shared__ int s_start[kExpertsLocal + 1];
-  if (threadIdx.x <= kExpertsLocal) s_start[threadIdx.x] = p.expert_start[threadIdx.x];
+  s_pre[j][e] = pre;
+  s_tot[j][e] = tot;
   __syncthreads();
-  const int s = blockIdx.x * kRouteTokensPerBlock * kTopK + threadIdx.x;
-  if (s >= p.T * kTopK) return;
-  const int le = local_of(p.topk_ids[s], p.offset);
+  if (tid < kExpertsLocal) {
+    int pe = 0, te = 0;
+#pragma unroll
+    for (int jj = 0; jj < kPlaceGroups; ++jj) {
+      pe += s_pre[jj][tid];
+      te += s_tot[jj][tid];
+    }
+    s_prefix[tid] = pe;
+    if (b == 0) {
+      finish_counts(p, tid, te, s_start);
+    } else {
+      int incl = te;
+#pragma unroll
+      for (int off = 1; off < kExpertsLocal; off <<= 1) {
+        const int o = __shfl_up(incl, off, kExpertsLocal);
+        if (tid >= off) incl += o;
+      }
+      s_start[tid + 1] = incl;
+      if (tid == 0) s_start[0] = 0;
+    }
+  }
+  __syncthreads();
   if (le < 0) return;
-  const int pos = s_start[le] + p.block_count[blockIdx.x * kExpertsLocal + le] + p.slot_rank[s];
+  const int pos = s_start[le] + s_prefix[le] + rank;
   p.sorted_token[pos] = s / kTopK;
-  p.sorted_weight[pos] = p.topk_w[s];
+  p.sorted_weight[pos] = w;
   p.sorted_slot[pos] = s;
 }
 
@@ -530,8 +542,7 @@ hipError_t launch_route_dispatch(const RouteParams& p, hipStream_t s) {
     hipLaunchKernelGGL(dispatch_small_kernel, dim3(1), dim3(kRouteThreads), 0, s, p);
   } else {
     hipLaunchKernelGGL(route_kernel<true>, dim3(p.nblocks), dim3(kRouteWaves * 64), 0, s, p);
-    hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(kRouteThreads), 0, s, p);
-    hipLaunchKernelGGL(place_kernel, dim3(p.nblocks), dim3(kRouteTokensPerBlock * kTopK), 0, s, p);
+    hipLaunchKernelGGL(place_kernel, dim3(p.nblocks), dim3(kPlaceThreads), 0, s, p);
   }
   return hipGetLastError();
 }
