@@ -69,6 +69,7 @@ extern "C" {
 #define MOE_FP8_EDEVICE            -7  /* current device is not gfx950 */
 #define MOE_FP8_EINVAL_HIDDEN_DTYPE -8 /* hidden_dtype of moe_fp8_quantize_hidden unknown */
 #define MOE_FP8_ESTATIC_TOKENS     -9  /* num_tokens > MOE_FP8_STATIC_MAX_TOKENS (moe_fp8_run_static) */
+#define MOE_FP8_EPACKED           -10  /* packed weights NULL or smaller than moe_fp8_packed_weights_bytes() */
 
 /* Largest num_tokens accepted: keeps every flat index (T*8*7168) inside int64 and
  * the per-token slot index inside int32. */
@@ -178,11 +179,36 @@ int moe_fp8_run(const moe_fp8_args* args, void* workspace, size_t workspace_byte
  * stage 1 (routing, and the dispatch above 64 tokens), events[1] before stage 2 (GEMM1, one
  * kernel; up to 64 tokens it also rebuilds the dispatch), events[2] before stage 3
  * (requantisation, GEMM2 and the combine) and events[3] after it. The events must have been
- * created by the caller (hipEventCreate) on the stream's device. Replaces run() (kernel.py:562-729)
- * like moe_fp8_run; the per-stage split mirrors its routing (:624-639), dispatch + GEMM1
- * (:649-693) and GEMM2 + finalize (:695-729) sections. */
-int moe_fp8_run_profiled(const moe_fp8_args* args, void* workspace, size_t workspace_bytes,
-                         hipStream_t stream, hipEvent_t events[4]);
+ * created by the caller (hipEventCreate) on the stream's device. With a non-NULL `packed` (the
+ * packed copy of args' weights, moe_fp8_pack_weights) it times moe_fp8_run_packed instead.
+ * Replaces run() (kernel.py:562-729) like moe_fp8_run; the per-stage split mirrors its routing
+ * (:624-639), dispatch + GEMM1 (:649-693) and GEMM2 + finalize (:695-729) sections. */
+int moe_fp8_run_profiled(const moe_fp8_args* args, const void* packed, size_t packed_bytes, void* workspace,
+                         size_t workspace_bytes, hipStream_t stream, hipEvent_t events[4]);
+
+/* A cached re-layout of the expert weights for the decode path, behind the same tensor
+ * contract: the caller keeps passing W13/W2 in their kernel.py:604-607 layout and may, once per
+ * weight set, build a packed copy that the GEMMs of batches up to 64 tokens stream instead.
+ * In the copy each wavefront's MFMA operand for a 128-wide K-step is contiguous (32 bytes per
+ * lane, 2 KB per 16-row fragment): W13 as blocks [expert][16 SwiGLU columns][K-step] of 4 KB
+ * (the gate rows' fragment, then the up rows'), then W2 as blocks [expert][16 hidden
+ * rows][K-step] of 2 KB; lane l of a fragment holds bytes [16(l/16), +16) and
+ * [64 + 16(l/16), +16) of the block's row l%16. Scales are not copied. An extension
+ * of the path with no counterpart in the reference, whose kernels read the weights row-major
+ * (kernel.py:91-102, 222-226). */
+#define MOE_FP8_PACKED_MAX_TOKENS 64          /* the largest batch that reads the packed copy */
+size_t moe_fp8_packed_weights_bytes(void);   /* 1,409,286,144: the size of W13 plus W2 */
+
+/* Writes the packed copy of args->gemm1_weights and args->gemm2_weights (only those two fields
+ * are read) into `packed` on `stream`. */
+int moe_fp8_pack_weights(const moe_fp8_args* args, void* packed, size_t packed_bytes, hipStream_t stream);
+
+/* moe_fp8_run with the packed copy of args' weights: up to 64 tokens GEMM1 and GEMM2 stream
+ * `packed` instead of args->gemm1_weights / gemm2_weights; above 64 tokens `packed` is not
+ * read. The output is bit-identical to moe_fp8_run's (the same arithmetic in the same order).
+ * Replaces run() (kernel.py:562-729) like moe_fp8_run. */
+int moe_fp8_run_packed(const moe_fp8_args* args, const void* packed, size_t packed_bytes, void* workspace,
+                       size_t workspace_bytes, hipStream_t stream);
 
 /* moe_fp8_run without a caller workspace, for callers that cannot allocate device memory
  * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). No
@@ -219,7 +245,7 @@ int moe_fp8_gemm1(const moe_fp8_args* args, void* workspace, size_t workspace_by
                   hipStream_t stream);
 
 /* Stage 3: (when layout.rows_per_item <= 32) requantisation of the fp32 SwiGLU rows to
- * act/act_scale; GEMM2 of act against the expert's down projection, weighting by the
+ * act/act_scale, one scale per layout.requant_block columns; GEMM2 of act against the expert's down projection, weighting by the
  * routing weight and the deterministic per-token combine into args->output (up to 64 tokens
  * in one kernel, above that a separate combine pass over the parked rows).
  * Replaces moe_gemm2_kernel and the finalize copy (kernel.py:695-729, 153-250). */

@@ -40,7 +40,9 @@ ELAUNCH = -6
 EDEVICE = -7
 EINVAL_HIDDEN_DTYPE = -8
 ESTATIC_TOKENS = -9
+EPACKED = -10
 STATIC_MAX_TOKENS = 64
+PACKED_MAX_TOKENS = 64
 STATIC_SCRATCH_BYTES = 6 << 20
 
 EXPORTED_SYMBOLS = (
@@ -50,6 +52,9 @@ EXPORTED_SYMBOLS = (
     "moe_fp8_run",
     "moe_fp8_run_profiled",
     "moe_fp8_run_static",
+    "moe_fp8_packed_weights_bytes",
+    "moe_fp8_pack_weights",
+    "moe_fp8_run_packed",
     "moe_fp8_route_dispatch",
     "moe_fp8_gemm1",
     "moe_fp8_gemm2_combine",
@@ -137,10 +142,16 @@ def load() -> ctypes.CDLL:
         lib.moe_fp8_workspace_init.restype = ctypes.c_int
         lib.moe_fp8_run.argtypes = [args_p, vp, sz, vp]
         lib.moe_fp8_run.restype = ctypes.c_int
-        lib.moe_fp8_run_profiled.argtypes = [args_p, vp, sz, vp, ctypes.POINTER(vp)]
+        lib.moe_fp8_run_profiled.argtypes = [args_p, vp, sz, vp, sz, vp, ctypes.POINTER(vp)]
         lib.moe_fp8_run_profiled.restype = ctypes.c_int
         lib.moe_fp8_run_static.argtypes = [args_p, vp]
         lib.moe_fp8_run_static.restype = ctypes.c_int
+        lib.moe_fp8_packed_weights_bytes.argtypes = []
+        lib.moe_fp8_packed_weights_bytes.restype = sz
+        lib.moe_fp8_pack_weights.argtypes = [args_p, vp, sz, vp]
+        lib.moe_fp8_pack_weights.restype = ctypes.c_int
+        lib.moe_fp8_run_packed.argtypes = [args_p, vp, sz, vp, sz, vp]
+        lib.moe_fp8_run_packed.restype = ctypes.c_int
         lib.moe_fp8_route_dispatch.argtypes = [args_p, i32, vp, sz, vp]
         lib.moe_fp8_route_dispatch.restype = ctypes.c_int
         lib.moe_fp8_gemm1.argtypes = [args_p, vp, sz, vp]
@@ -174,3 +185,7 @@ def workspace_layout(num_tokens: int) -> MoeFp8Layout:
 
 def workspace_bytes(num_tokens: int) -> int:
     return int(load().moe_fp8_workspace_bytes(int(num_tokens)))
+
+
+def packed_weights_bytes() -> int:
+    return int(load().moe_fp8_packed_weights_bytes())

@@ -170,26 +170,34 @@ namespace {
 // The launch sequence of moe_fp8_run; with `events`, events[i] is recorded on the stream
 // before stage i+1 (routing [+ dispatch], GEMM1, requantisation + GEMM2 + combine) and
 // events[3] after the last launch.
+// packed: the packed copy of W13 and W2 (moe_fp8_pack_weights) or null; read only up to 64
+// tokens, where the decode kernels stream it instead of args' weights.
 int run_layer(const moe_fp8_args* args, void* workspace, size_t workspace_bytes, hipStream_t stream,
-              hipEvent_t* events) {
+              hipEvent_t* events, const uint8_t* packed = nullptr) {
   moe_fp8_layout L;
   const int rc = check_args(args, true, workspace, workspace_bytes, &L);
   if (rc != MOE_FP8_OK) return rc;
   if (args->num_tokens == 0) return MOE_FP8_OK;
   const RouteParams rp = route_params(args, L, workspace, 0);
-  const GemmParams gp = gemm_params(args, L, workspace);
+  GemmParams gp = gemm_params(args, L, workspace);
+  static_assert(MOE_FP8_PACKED_MAX_TOKENS == kFusedDispatchTokens, "the decode kernels read the packed copy");
+  const bool use_packed = packed && args->num_tokens <= MOE_FP8_PACKED_MAX_TOKENS;
+  if (use_packed) {
+    gp.w13 = packed;
+    gp.w2 = packed + (packed_weights_bytes() - (size_t)kExpertsLocal * kHidden * kInter);
+  }
   auto mark = [&](int i) { return !events || hipEventRecord(events[i], stream) == hipSuccess; };
   if (!mark(0)) return MOE_FP8_ELAUNCH;
   if (args->num_tokens <= kFusedDispatchTokens) {
     // routing, then GEMM1 with the dispatch rebuilt in every work-group: one launch less
     if (launch_route(rp, stream) != hipSuccess || !mark(1)) return MOE_FP8_ELAUNCH;
-    if (launch_gemm1_dispatch(gp, rp, stream) != hipSuccess || !mark(2)) return MOE_FP8_ELAUNCH;
+    if (launch_gemm1_dispatch(gp, rp, use_packed, stream) != hipSuccess || !mark(2)) return MOE_FP8_ELAUNCH;
   } else {
     if (launch_route_dispatch(rp, stream) != hipSuccess || !mark(1)) return MOE_FP8_ELAUNCH;
     if (launch_gemm1(gp, L.rows_per_item, stream) != hipSuccess || !mark(2)) return MOE_FP8_ELAUNCH;
   }
   if (launch_requant(gp, L.rows_per_item, stream) != hipSuccess) return MOE_FP8_ELAUNCH;
-  if (launch_gemm2(gp, L.rows_per_item, stream) != hipSuccess) return MOE_FP8_ELAUNCH;
+  if (launch_gemm2(gp, L.rows_per_item, use_packed, stream) != hipSuccess) return MOE_FP8_ELAUNCH;
   if (launch_combine(gp, L.rows_per_item, stream) != hipSuccess || !mark(3)) return MOE_FP8_ELAUNCH;
   return MOE_FP8_OK;
 }
@@ -274,7 +282,7 @@ int moe_fp8_gemm2_combine(const moe_fp8_args* args, void* workspace, size_t work
   if (args->num_tokens == 0) return MOE_FP8_OK;
   const GemmParams p = gemm_params(args, L, workspace);
   if (launch_requant(p, L.rows_per_item, stream) != hipSuccess) return MOE_FP8_ELAUNCH;
-  if (launch_gemm2(p, L.rows_per_item, stream) != hipSuccess) return MOE_FP8_ELAUNCH;
+  if (launch_gemm2(p, L.rows_per_item, false, stream) != hipSuccess) return MOE_FP8_ELAUNCH;
   return launch_combine(p, L.rows_per_item, stream) == hipSuccess ? MOE_FP8_OK : MOE_FP8_ELAUNCH;
 }
 
@@ -284,10 +292,30 @@ int moe_fp8_run(const moe_fp8_args* args, void* workspace, size_t workspace_byte
   return run_layer(args, workspace, workspace_bytes, stream, nullptr);
 }
 
-int moe_fp8_run_profiled(const moe_fp8_args* args, void* workspace, size_t workspace_bytes,
-                         hipStream_t stream, hipEvent_t events[4]) {
+int moe_fp8_run_profiled(const moe_fp8_args* args, const void* packed, size_t packed_bytes, void* workspace,
+                         size_t workspace_bytes, hipStream_t stream, hipEvent_t events[4]) {
   if (!events || !events[0] || !events[1] || !events[2] || !events[3]) return MOE_FP8_EINVAL_POINTER;
-  return run_layer(args, workspace, workspace_bytes, stream, events);
+  if (packed && packed_bytes < packed_weights_bytes()) return MOE_FP8_EPACKED;
+  return run_layer(args, workspace, workspace_bytes, stream, events, static_cast<const uint8_t*>(packed));
+}
+
+size_t moe_fp8_packed_weights_bytes(void) { return packed_weights_bytes(); }
+
+int moe_fp8_pack_weights(const moe_fp8_args* args, void* packed, size_t packed_bytes, hipStream_t stream) {
+  if (!args || !args->gemm1_weights || !args->gemm2_weights) return MOE_FP8_EINVAL_POINTER;
+  if (!packed || packed_bytes < packed_weights_bytes()) return MOE_FP8_EPACKED;
+  const int rc = check_device();
+  if (rc != MOE_FP8_OK) return rc;
+  return launch_pack_weights(args->gemm1_weights, args->gemm2_weights, static_cast<uint8_t*>(packed), stream) ==
+                 hipSuccess
+             ? MOE_FP8_OK
+             : MOE_FP8_ELAUNCH;
+}
+
+int moe_fp8_run_packed(const moe_fp8_args* args, const void* packed, size_t packed_bytes, void* workspace,
+                       size_t workspace_bytes, hipStream_t stream) {
+  if (!packed || packed_bytes < packed_weights_bytes()) return MOE_FP8_EPACKED;
+  return run_layer(args, workspace, workspace_bytes, stream, nullptr, static_cast<const uint8_t*>(packed));
 }
 
 int moe_fp8_run_static(const moe_fp8_args* args, hipStream_t stream) {
@@ -328,6 +356,7 @@ const char* moe_fp8_strerror(int code) {
     case MOE_FP8_ELAUNCH: return "a HIP kernel launch failed";
     case MOE_FP8_EDEVICE: return "the current HIP device is not a gfx950 (MI355X) GPU";
     case MOE_FP8_EINVAL_HIDDEN_DTYPE: return "hidden_dtype must be MOE_FP8_HIDDEN_F32, _BF16 or _F16";
+    case MOE_FP8_EPACKED: return "packed weights are NULL or smaller than moe_fp8_packed_weights_bytes()";
     case MOE_FP8_ESTATIC_TOKENS:
       return "num_tokens exceeds MOE_FP8_STATIC_MAX_TOKENS (64), the largest batch moe_fp8_run_static's "
              "built-in workspace holds; use moe_fp8_run with a caller workspace";

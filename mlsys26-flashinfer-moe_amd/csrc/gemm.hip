@@ -74,6 +74,20 @@ __device__ __forceinline__ v8i load_frag(const uint8_t* p) {
   return join(lo, hi);
 }
 
+// The same fragment from the packed copy of the weights (moe_fp8_pack_weights), where each
+// lane's 32 bytes of a K-step are contiguous (p already points at the lane's 32 bytes).
+__device__ __forceinline__ v8i load_frag_packed(const uint8_t* p) {
+  const v4i lo = *reinterpret_cast<const v4i*>(p);
+  const v4i hi = *reinterpret_cast<const v4i*>(p + 16);
+  return join(lo, hi);
+}
+
+// Packed weights (decode kernels): W13 in blocks [expert][16-column slice][K-step] of 4096 bytes,
+// the gate fragment then the up fragment; W2 in blocks [expert][16 hidden rows][K-step] of 2048
+// bytes. A fragment is 64 lanes x 32 bytes in the order load_frag gives them.
+constexpr size_t kPackedFrag = 64 * 32;
+constexpr size_t kPackedW13Bytes = (size_t)kExpertsLocal * 2 * kInter * kHidden;
+
 template <int NF, int NG>
 struct StreamStage {
   v8i w[NF];
@@ -87,10 +101,12 @@ struct StreamStage {
 // readlane, so the loop holds no branches and the compiler's waits cover exactly the step
 // being consumed. Lane l ends with rows 4*(l/16)+i of each weight fragment against row
 // l%16 of each row group.
-template <int KIND, int NG>
+// With PACKED (GEMM1 only) the weights come from the packed copy.
+template <int KIND, int NG, bool PACKED = false>
 __device__ __forceinline__ void stream_accumulate(const GemmParams& p, int e, int r0, int rows, int slice,
                                                   int lane, const int32_t* row_token,
                                                   v4f (&acc)[StreamShape<KIND>::kFrags][NG]) {
+  static_assert(!PACKED || KIND == kG1, "packed weights: GEMM1 of the decode path");
   using S = StreamShape<KIND>;
   constexpr int KS = S::kSteps;
   constexpr int NF = S::kFrags;
@@ -103,8 +119,13 @@ __device__ __forceinline__ void stream_accumulate(const GemmParams& p, int e, in
   float sw_lane[NF];
   if constexpr (KIND == kG1) {
     const int row = slice * 16 + (lane & 15);                 // gate row; up row = + I
-    wf[0] = p.w13 + ((size_t)e * 2 * kInter + row) * kHidden + (lane >> 4) * 16;
-    wf[1] = wf[0] + (size_t)kInter * kHidden;
+    if constexpr (PACKED) {
+      wf[0] = p.w13 + ((size_t)e * S::kSlices + slice) * KS * 2 * kPackedFrag + lane * 32;
+      wf[1] = wf[0] + kPackedFrag;
+    } else {
+      wf[0] = p.w13 + ((size_t)e * 2 * kInter + row) * kHidden + (lane >> 4) * 16;
+      wf[1] = wf[0] + (size_t)kInter * kHidden;
+    }
     sw_lane[0] = p.w13_scale[((size_t)e * 32 + slice / 8) * kHBlocks + (lane < KS ? lane : 0)];
     sw_lane[1] = p.w13_scale[((size_t)e * 32 + kIBlocks + slice / 8) * kHBlocks + (lane < KS ? lane : 0)];
   } else {
@@ -117,13 +138,16 @@ __device__ __forceinline__ void stream_accumulate(const GemmParams& p, int e, in
     for (int f = 0; f < NF; ++f) sw_lane[f] = sw;
   }
 
+  // one K-step further along a weight fragment
+  constexpr size_t kWStep = PACKED ? 2 * kPackedFrag : 128;
+  auto wload = [&](const uint8_t* q) { return PACKED ? load_frag_packed(q) : load_frag(q); };
   StreamStage<NF, NG> ring[NB];
   // the weight loads of the first steps go out before the activation addresses are known
   // (GEMM1 reads them from sorted_token, one more memory round trip)
 #pragma unroll
   for (int s = 0; s < NB - 1; ++s)
 #pragma unroll
-    for (int f = 0; f < NF; ++f) ring[s].w[f] = load_frag(wf[f] + s * 128);
+    for (int f = 0; f < NF; ++f) ring[s].w[f] = wload(wf[f] + s * kWStep);
 
   // activation rows of this lane's column in each 16-row group (rows past the item's end
   // read its first row; their results are never stored)
@@ -153,7 +177,7 @@ __device__ __forceinline__ void stream_accumulate(const GemmParams& p, int e, in
   };
   auto issue = [&](int k, StreamStage<NF, NG>& st) {
 #pragma unroll
-    for (int f = 0; f < NF; ++f) st.w[f] = load_frag(wf[f] + k * 128);
+    for (int f = 0; f < NF; ++f) st.w[f] = wload(wf[f] + k * kWStep);
     issue_a(k, st);
   };
 #pragma unroll
@@ -202,12 +226,12 @@ __device__ __forceinline__ v4f swiglu4(const v4f& x1, const v4f& x2) {
 
 // One work unit with its epilogue: GEMM1 writes fp32 SwiGLU rows for requant_kernel; GEMM2
 // writes or parks the weighted rows.
-template <int KIND, int NG>
+template <int KIND, int NG, bool PACKED = false>
 __device__ __forceinline__ void stream_unit(const GemmParams& p, int e, int r0, int rows, int slice, int lane,
                                             const int32_t* row_token) {
   constexpr int NF = StreamShape<KIND>::kFrags;
   v4f acc[NF][NG];
-  stream_accumulate<KIND, NG>(p, e, r0, rows, slice, lane, row_token, acc);
+  stream_accumulate<KIND, NG, PACKED>(p, e, r0, rows, slice, lane, row_token, acc);
   // lane: column (lane & 15) of each row group, fragment rows 4*(lane>>4) + i
 #pragma unroll
   for (int g = 0; g < NG; ++g) {
@@ -242,7 +266,7 @@ __device__ __forceinline__ void stream_unit(const GemmParams& p, int e, int r0, 
 
 // The work units of n_items items (item list and GEMM1's bucket-row -> token map in the
 // workspace, or in LDS for the fused dispatch below).
-template <int KIND, int MAXNG>
+template <int KIND, int MAXNG, bool PACKED = false>
 __device__ __forceinline__ void stream_units(const GemmParams& p, int n_items, const int4* items,
                                              const int32_t* row_token) {
   constexpr int SL = StreamShape<KIND>::kSlices;
@@ -258,8 +282,8 @@ __device__ __forceinline__ void stream_units(const GemmParams& p, int n_items, c
     const int e = __builtin_amdgcn_readfirstlane(it.x);
     const int r0 = __builtin_amdgcn_readfirstlane(it.y);
     const int rows = __builtin_amdgcn_readfirstlane(it.z);
-    if (MAXNG == 1 || rows <= 16) stream_unit<KIND, 1>(p, e, r0, rows, slice, lane, row_token);
-    else stream_unit<KIND, MAXNG>(p, e, r0, rows, slice, lane, row_token);
+    if (MAXNG == 1 || rows <= 16) stream_unit<KIND, 1, PACKED>(p, e, r0, rows, slice, lane, row_token);
+    else stream_unit<KIND, MAXNG, PACKED>(p, e, r0, rows, slice, lane, row_token);
   }
 }
 
@@ -391,10 +415,12 @@ __device__ __forceinline__ void fused_dispatch(const GemmParams& p, const RouteP
   __syncthreads();
 }
 
+// PACKED: p.w13 is the packed copy of W13 (moe_fp8_run_packed).
+template <bool PACKED>
 __global__ __launch_bounds__(kStreamWaves * 64) void gemm1_stream_dispatch_kernel(GemmParams p, RouteParams rp) {
   __shared__ FusedDispatch s;
   fused_dispatch(p, rp, s);
-  stream_units<kG1, 1>(p, s.n_items, s.items, s.row_token);
+  stream_units<kG1, 1, PACKED>(p, s.n_items, s.items, s.row_token);
 }
 
 // Requantises the fp32 SwiGLU rows: per row and COLS columns, scale = max(amax/448, 1e-12)
@@ -457,6 +483,8 @@ struct SliceStage {
   float wt;         // routing weight of the lane's row
 };
 
+// PACKED: p.w2 is the packed copy of W2 (moe_fp8_run_packed).
+template <bool PACKED>
 __global__ __launch_bounds__(kSliceQuarters * 64) void gemm2_slice_kernel(GemmParams p) {
   __shared__ __attribute__((aligned(16))) float acc_lds[kSliceQuarters][kFusedDispatchTokens][16 * kSliceF];
   const int lane = threadIdx.x & 63;
@@ -483,8 +511,13 @@ __global__ __launch_bounds__(kSliceQuarters * 64) void gemm2_slice_kernel(GemmPa
         const int rows = __builtin_amdgcn_readlane(my_item.z, it);
         const int r = r0 + (m < rows ? m : 0);
 #pragma unroll
-        for (int f = 0; f < kSliceF; ++f)
-          g.w[f] = load_frag(p.w2 + ((size_t)e * kHidden + h0 + 16 * f + m) * kInter + ks * 128 + (lane >> 4) * 16);
+        for (int f = 0; f < kSliceF; ++f) {
+          if constexpr (PACKED)
+            g.w[f] = load_frag_packed(p.w2 + (((size_t)e * (kHidden / 16) + (h0 >> 4) + f) * kIBlocks + ks) * kPackedFrag +
+                                      lane * 32);
+          else
+            g.w[f] = load_frag(p.w2 + ((size_t)e * kHidden + h0 + 16 * f + m) * kInter + ks * 128 + (lane >> 4) * 16);
+        }
         g.a = load_frag(p.act + (size_t)r * kInter + ks * 128 + (lane >> 4) * 16);
         g.sa = *reinterpret_cast<const float2*>(p.act_scale + (size_t)r * kQuantBlocks + 2 * ks);
         g.sw = p.w2_scale[((size_t)e * kHBlocks + h0 / 128) * kIBlocks + ks];
@@ -683,20 +716,63 @@ hipError_t launch_stream(const GemmParams& p, int rows_per_item, hipStream_t s) 
   return rows_per_item <= 16 ? launch_stream_ng<KIND, 1>(p, s) : launch_stream_ng<KIND, 2>(p, s);
 }
 
+// Writes the packed copy of W13 and W2: one 16-byte chunk per thread and iteration, in the
+// packed order (the reads gather 16-byte pieces of rows; a one-time conversion).
+__global__ __launch_bounds__(256) void pack_weights_kernel(const uint8_t* __restrict__ w13, const uint8_t* __restrict__ w2,
+                                                           uint8_t* __restrict__ packed) {
+  constexpr size_t kChunks13 = kPackedW13Bytes / 16;
+  constexpr size_t kChunks = kChunks13 + (size_t)kExpertsLocal * kHidden * kInter / 16;
+  constexpr int kSlices1 = kInter / 16;
+  for (size_t c = (size_t)blockIdx.x * blockDim.x + threadIdx.x; c < kChunks; c += (size_t)gridDim.x * blockDim.x) {
+    const size_t o = c * 16;   // byte offset in the packed copy
+    const int half = (int)(o >> 4) & 1;
+    const int lane = (int)(o >> 5) & 63;
+    const int col16 = (lane >> 4) * 16 + half * 64;   // byte of the 128-byte K block
+    const uint8_t* src;
+    if (c < kChunks13) {
+      const size_t blk = o / (2 * kPackedFrag);       // (expert, slice, K-step)
+      const int f = (int)(o / kPackedFrag) & 1;       // gate, up
+      const int k = (int)(blk % kHBlocks);
+      const int slice = (int)((blk / kHBlocks) % kSlices1);
+      const int e = (int)(blk / ((size_t)kHBlocks * kSlices1));
+      const int row = f * kInter + slice * 16 + (lane & 15);
+      src = w13 + ((size_t)e * 2 * kInter + row) * kHidden + k * 128 + col16;
+    } else {
+      const size_t o2 = o - kPackedW13Bytes;
+      const size_t blk = o2 / kPackedFrag;            // (expert, 16 hidden rows, K-step)
+      const int k = (int)(blk % kIBlocks);
+      const int h = (int)((blk / kIBlocks) % (kHidden / 16));
+      const int e = (int)(blk / ((size_t)kIBlocks * (kHidden / 16)));
+      src = w2 + ((size_t)e * kHidden + h * 16 + (lane & 15)) * kInter + k * 128 + col16;
+    }
+    *reinterpret_cast<v4i*>(packed + o) = *reinterpret_cast<const v4i*>(src);
+  }
+}
+
 }  // namespace
+
+size_t packed_weights_bytes() { return kPackedW13Bytes + (size_t)kExpertsLocal * kHidden * kInter; }
+
+hipError_t launch_pack_weights(const uint8_t* w13, const uint8_t* w2, uint8_t* packed, hipStream_t s) {
+  hipLaunchKernelGGL(pack_weights_kernel, dim3(num_cus() * 8), dim3(256), 0, s, w13, w2, packed);
+  return hipGetLastError();
+}
 
 hipError_t launch_gemm1(const GemmParams& p, int rows_per_item, hipStream_t s) {
   if (rows_per_item > 32) return launch_gemm1_tile(p, rows_per_item, s);
   return launch_stream<kG1>(p, rows_per_item, s);
 }
 
-hipError_t launch_gemm1_dispatch(const GemmParams& p, const RouteParams& rp, hipStream_t s) {
+hipError_t launch_gemm1_dispatch(const GemmParams& p, const RouteParams& rp, bool packed, hipStream_t s) {
   static int occ = 0;
   if (p.T <= 0 || p.T > kFusedDispatchTokens || rp.rows_per_item != kFusedItemRows) return hipErrorInvalidValue;
-  int grid = num_cus() * resident_per_cu(gemm1_stream_dispatch_kernel, occ);
+  int grid = num_cus() * resident_per_cu(gemm1_stream_dispatch_kernel<false>, occ);
   const int cap = (kFusedItems * StreamShape<kG1>::kSlices + kStreamWaves - 1) / kStreamWaves;
   if (grid > cap) grid = cap;
-  hipLaunchKernelGGL(gemm1_stream_dispatch_kernel, dim3(grid), dim3(kStreamWaves * 64), 0, s, p, rp);
+  if (packed)
+    hipLaunchKernelGGL(gemm1_stream_dispatch_kernel<true>, dim3(grid), dim3(kStreamWaves * 64), 0, s, p, rp);
+  else
+    hipLaunchKernelGGL(gemm1_stream_dispatch_kernel<false>, dim3(grid), dim3(kStreamWaves * 64), 0, s, p, rp);
   return hipGetLastError();
 }
 
@@ -712,12 +788,13 @@ hipError_t launch_requant(const GemmParams& p, int rows_per_item, hipStream_t s)
   return hipGetLastError();
 }
 
-hipError_t launch_gemm2(const GemmParams& p, int rows_per_item, hipStream_t s) {
+hipError_t launch_gemm2(const GemmParams& p, int rows_per_item, bool packed, hipStream_t s) {
   if (rows_per_item > 32) return launch_gemm2_tile(p, rows_per_item, s);
   if (rows_per_item == kFusedItemRows) {
     // up to 64 tokens: GEMM2 with the combine, one work-group per 32-row hidden slice
     if (p.T > kFusedDispatchTokens) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(gemm2_slice_kernel, dim3(kHiddenSlices), dim3(kSliceQuarters * 64), 0, s, p);
+    if (packed) hipLaunchKernelGGL(gemm2_slice_kernel<true>, dim3(kHiddenSlices), dim3(kSliceQuarters * 64), 0, s, p);
+    else hipLaunchKernelGGL(gemm2_slice_kernel<false>, dim3(kHiddenSlices), dim3(kSliceQuarters * 64), 0, s, p);
     return hipGetLastError();
   }
   return launch_stream<kG2>(p, rows_per_item, s);

@@ -132,9 +132,14 @@ struct GemmParams {
 hipError_t launch_route_dispatch(const RouteParams& p, hipStream_t s);
 hipError_t launch_route(const RouteParams& p, hipStream_t s);
 hipError_t launch_gemm1(const GemmParams& p, int rows_per_item, hipStream_t s);
-hipError_t launch_gemm1_dispatch(const GemmParams& p, const RouteParams& rp, hipStream_t s);
+// packed: p.w13 is the packed copy of W13 (moe_fp8_pack_weights).
+hipError_t launch_gemm1_dispatch(const GemmParams& p, const RouteParams& rp, bool packed, hipStream_t s);
 hipError_t launch_requant(const GemmParams& p, int rows_per_item, hipStream_t s);
-hipError_t launch_gemm2(const GemmParams& p, int rows_per_item, hipStream_t s);
+// packed (16-row items only): p.w2 is the packed copy of W2.
+hipError_t launch_gemm2(const GemmParams& p, int rows_per_item, bool packed, hipStream_t s);
+// The packed copy of W13 and W2 read by the decode kernels (moe_fp8_pack_weights).
+size_t packed_weights_bytes();
+hipError_t launch_pack_weights(const uint8_t* w13, const uint8_t* w2, uint8_t* packed, hipStream_t s);
 hipError_t launch_combine(const GemmParams& p, int rows_per_item, hipStream_t s);
 hipError_t launch_gemm1_tile(const GemmParams& p, int rows_per_item, hipStream_t s);
 hipError_t launch_quantize_hidden(const void* x, int dtype, int T, uint8_t* q, float* scale, hipStream_t s);

@@ -14,7 +14,7 @@ import torch
 from . import _lib
 from ._lib import (BIAS_BF16, BIAS_F16, BIAS_F32, EXPERTS_GLOBAL, EXPERTS_LOCAL, G1_BLOCKS,
                    H_BLOCKS, HIDDEN, HIDDEN_BF16, HIDDEN_F16, HIDDEN_F32, I_BLOCKS, INTER, OUT_BF16,
-                   OUT_F32)
+                   OUT_F32, PACKED_MAX_TOKENS)
 
 _BIAS_CODES = {torch.float32: BIAS_F32, torch.bfloat16: BIAS_BF16, torch.float16: BIAS_F16}
 
@@ -146,6 +146,96 @@ def workspace_for(num_tokens: int, device: torch.device) -> Workspace:
     return _workspaces.get(key, num_tokens, _lib.workspace_bytes(num_tokens), device, stream)
 
 
+class PackedWeightCache:
+    """Packed copies of weight sets (pack_weights) that run() streams up to 64 tokens.
+
+    The weights keep their kernel.py:604-607 contract: run() receives them row-major as ever,
+    and the first call of up to 64 tokens with a weight set builds its packed copy (one kernel
+    on the current stream, 1.41 GB), which later calls with the same set stream instead. A copy
+    belongs to the weights' storage (W13's and W2's device addresses, held by weak reference) and
+    to their version counters: modifying the weights in place through torch, or freeing them and
+    allocating new ones at the same address, makes the copy stale, and the next call replaces it.
+    Writes to the weights that bypass torch (raw pointers) are not seen: call clear() then.
+
+    At most `max_sets` copies are held; further weight sets run on the row-major weights (no
+    eviction, so that a model with more layers than copies never repacks in a loop). No copy is
+    built while the current stream is being captured into a HIP graph; a copy that a capture has
+    used is never freed (a stale one moves to a retired list), because the graph holds its
+    address. `make(w13, w2)` and `capturing()` are injectable so that the policy is testable
+    without a GPU.
+    """
+
+    def __init__(self, max_sets: int = 4, make=None, capturing=None, storage_ref=None):
+        from torch.multiprocessing.reductions import StorageWeakRef
+        self.max_sets = max_sets
+        self._make = make or (lambda w13, w2: pack_weights(w13, w2))
+        self._capturing = capturing or torch.cuda.is_current_stream_capturing
+        self._ref = storage_ref or (lambda t: StorageWeakRef(t.untyped_storage()))
+        self._lock = threading.Lock()
+        self._entries = {}
+        self._retired = []
+
+    def get(self, w13: torch.Tensor, w2: torch.Tensor):
+        """The packed copy for (w13, w2), built if missing or stale; None when the set does
+        not fit or the stream is being captured without a copy."""
+        if self.max_sets <= 0:
+            return None
+        key = (w13.device.index, w13.data_ptr(), w2.data_ptr())
+        version = (w13._version, w2._version)
+        with self._lock:
+            capturing = self._capturing()
+            ent = self._entries.get(key)
+            if ent is not None and not ent["ref13"].expired() and not ent["ref2"].expired() \
+                    and ent["version"] == version:
+                ent["captured"] = ent["captured"] or capturing
+                return ent["packed"]
+            if capturing:
+                return None
+            if ent is not None:
+                self._drop(key)
+            for k in [k for k, v in self._entries.items() if v["ref13"].expired() or v["ref2"].expired()]:
+                self._drop(k)
+            if len(self._entries) >= self.max_sets:
+                return None
+            packed = self._make(w13, w2)
+            self._entries[key] = dict(ref13=self._ref(w13), ref2=self._ref(w2), version=version, packed=packed,
+                                      captured=False)
+            return packed
+
+    def _drop(self, key):
+        ent = self._entries.pop(key)
+        if ent["captured"]:
+            self._retired.append(ent["packed"])
+
+    def clear(self):
+        """Forgets every copy (copies a graph capture used are kept alive in the retired list)."""
+        with self._lock:
+            for k in list(self._entries):
+                self._drop(k)
+
+    def __len__(self) -> int:
+        return len(self._entries)
+
+    @property
+    def retired(self) -> list:
+        return list(self._retired)
+
+
+_packed_weights = PackedWeightCache()
+
+
+def packed_weights_for(gemm1_weights: torch.Tensor, gemm2_weights: torch.Tensor):
+    """The packed copy run() uses for this weight set (built now if missing), or None when the
+    cache is off or full."""
+    return _packed_weights.get(gemm1_weights, gemm2_weights)
+
+
+def set_packed_weight_sets(max_sets: int) -> None:
+    """How many weight sets run() keeps a packed copy of (default 4, 1.41 GB each); 0 turns the
+    packed path of run() off. Copies already built are kept (see PackedWeightCache.clear)."""
+    _packed_weights.max_sets = int(max_sets)
+
+
 def make_args(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
               gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, local_expert_offset,
               routed_scaling_factor, output) -> _lib.MoeFp8Args:
@@ -189,7 +279,60 @@ def run(
     contribution, weighted by the renormalised routing weights) is written into
     `output` [T, 7168]. A bf16 or fp32 `output` on the GPU is written directly by the
     kernels; any other dtype or device receives a copy_ of a bf16 result.
+
+    Up to 64 tokens, with contiguous weights already on the GPU, the GEMMs stream a packed copy
+    of the weight set that the first such call builds and later calls reuse (PackedWeightCache;
+    set_packed_weight_sets(0) turns it off). The output is bit-identical either way.
     """
+    _run(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights, gemm1_weights_scale,
+         gemm2_weights, gemm2_weights_scale, local_expert_offset, routed_scaling_factor, output, _AUTO)
+    return None
+
+
+_AUTO = object()   # run(): the packed copy from the cache, when one applies
+
+
+@torch.no_grad()
+def pack_weights(gemm1_weights: torch.Tensor, gemm2_weights: torch.Tensor) -> torch.Tensor:
+    """The packed copy of W13 and W2 that the decode GEMMs stream (moe_fp8_pack_weights): a uint8
+    tensor of moe_fp8_packed_weights_bytes() on the weights' device, to be kept with the weight
+    set and passed to run_packed. The weights keep their kernel.py:604-607 contract."""
+    assert gemm1_weights.dtype == torch.float8_e4m3fn and tuple(gemm1_weights.shape) == (EXPERTS_LOCAL, 2 * INTER, HIDDEN), \
+        "gemm1_weights must be float8_e4m3fn [32, 4096, 7168]"
+    assert gemm2_weights.dtype == torch.float8_e4m3fn and tuple(gemm2_weights.shape) == (EXPERTS_LOCAL, HIDDEN, INTER), \
+        "gemm2_weights must be float8_e4m3fn [32, 7168, 2048]"
+    if not (gemm1_weights.is_cuda and gemm2_weights.is_cuda) or gemm1_weights.device != gemm2_weights.device:
+        raise RuntimeError("pack_weights needs both weight tensors on one GPU")
+    dev = gemm1_weights.device
+    lib = _lib.load()
+    w13, w2 = gemm1_weights.contiguous(), gemm2_weights.contiguous()
+    packed = torch.empty(_lib.packed_weights_bytes(), dtype=torch.uint8, device=dev)
+    args = _lib.MoeFp8Args()
+    args.gemm1_weights = w13.data_ptr()
+    args.gemm2_weights = w2.data_ptr()
+    with torch.cuda.device(dev):
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        _lib.check(lib.moe_fp8_pack_weights(args, packed.data_ptr(), packed.numel(), stream),
+                   "moe_fp8_pack_weights")
+    return packed
+
+
+@torch.no_grad()
+def run_packed(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
+               gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, local_expert_offset: int,
+               routed_scaling_factor: float, output: torch.Tensor, *, packed_weights: torch.Tensor):
+    """run() with the packed copy of this weight set (pack_weights): up to 64 tokens the GEMMs
+    stream `packed_weights` instead of gemm1_weights / gemm2_weights; the output is bit-identical
+    to run()'s."""
+    assert packed_weights.dtype == torch.uint8 and packed_weights.is_contiguous() and \
+        packed_weights.numel() >= _lib.packed_weights_bytes(), "packed_weights must come from pack_weights"
+    _run(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights, gemm1_weights_scale,
+         gemm2_weights, gemm2_weights_scale, local_expert_offset, routed_scaling_factor, output, packed_weights)
+    return None
+
+
+def _run(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights, gemm1_weights_scale,
+         gemm2_weights, gemm2_weights_scale, local_expert_offset, routed_scaling_factor, output, packed):
     T = validate(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
                  gemm1_weights_scale, gemm2_weights, gemm2_weights_scale)
     assert tuple(output.shape) == (T, HIDDEN), "output must be [T, 7168]"
@@ -220,10 +363,18 @@ def run(
         args = make_args(logits, bias, hidden, hidden_scale, w13, w13_scale, w2, w2_scale,
                          local_expert_offset, routed_scaling_factor, dst)
         stream = torch.cuda.current_stream(dev).cuda_stream
-        _lib.check(lib.moe_fp8_run(args, ws.ptr, ws.buffer.numel(), stream), "moe_fp8_run")
+        if packed is _AUTO:
+            packed = _packed_weights.get(w13, w2) if (
+                T <= PACKED_MAX_TOKENS and w13 is gemm1_weights and w2 is gemm2_weights) else None
+        if packed is None:
+            _lib.check(lib.moe_fp8_run(args, ws.ptr, ws.buffer.numel(), stream), "moe_fp8_run")
+        else:
+            if packed.device != dev:
+                raise RuntimeError(f"packed_weights must be on {dev}; got {packed.device}")
+            _lib.check(lib.moe_fp8_run_packed(args, packed.data_ptr(), packed.numel(), ws.ptr, ws.buffer.numel(),
+                                              stream), "moe_fp8_run_packed")
     if not direct:
         output.copy_(dst)
-    return None
 
 
 _HIDDEN_CODES = {torch.float32: HIDDEN_F32, torch.bfloat16: HIDDEN_BF16, torch.float16: HIDDEN_F16}

@@ -30,7 +30,8 @@ def test_constants_match_header(pkg):
     assert int(vals["MOE_FP8_HIDDEN"]) == L.HIDDEN and int(vals["MOE_FP8_INTER"]) == L.INTER
     assert int(vals["MOE_FP8_EXPERTS_LOCAL"]) == L.EXPERTS_LOCAL
     for name in ("OK", "EINVAL_POINTER", "EINVAL_TOKENS", "EWORKSPACE", "EINVAL_BIAS_DTYPE",
-                 "EINVAL_OUT_DTYPE", "ELAUNCH", "EDEVICE", "EINVAL_HIDDEN_DTYPE"):
+                 "EINVAL_OUT_DTYPE", "ELAUNCH", "EDEVICE", "EINVAL_HIDDEN_DTYPE", "ESTATIC_TOKENS", "EPACKED",
+                 "STATIC_MAX_TOKENS", "PACKED_MAX_TOKENS"):
         assert int(vals["MOE_FP8_" + name]) == getattr(L, name)
     for name in ("HIDDEN_F32", "HIDDEN_BF16", "HIDDEN_F16", "BIAS_F32", "BIAS_BF16", "BIAS_F16"):
         assert int(vals["MOE_FP8_" + name]) == getattr(L, name)
@@ -116,16 +117,40 @@ def test_argument_errors_are_reported_before_any_launch(pkg, lib):
     # the evented variant: all four events are required, and argument errors come first
     a = _args(pkg)
     ev = (ctypes.c_void_p * 4)(0x10, 0x20, 0x30, 0x40)
-    assert lib.moe_fp8_run_profiled(ctypes.byref(a), 0x1000, big, None, None) == L.EINVAL_POINTER
-    assert lib.moe_fp8_run_profiled(ctypes.byref(a), 0x1000, big, None,
+    assert lib.moe_fp8_run_profiled(ctypes.byref(a), None, 0, 0x1000, big, None, None) == L.EINVAL_POINTER
+    assert lib.moe_fp8_run_profiled(ctypes.byref(a), None, 0, 0x1000, big, None,
                                     (ctypes.c_void_p * 4)(0x10, 0x20, None, 0x40)) == L.EINVAL_POINTER
-    assert lib.moe_fp8_run_profiled(ctypes.byref(a), 0x1000, big - 1, None, ev) == L.EWORKSPACE
+    assert lib.moe_fp8_run_profiled(ctypes.byref(a), None, 0, 0x1000, big - 1, None, ev) == L.EWORKSPACE
+    assert lib.moe_fp8_run_profiled(ctypes.byref(a), 0x1000, 4096, 0x1000, big, None, ev) == L.EPACKED
     # T = 0 is a no-op that succeeds without a device
     a = _args(pkg, 0)
     assert lib.moe_fp8_run(ctypes.byref(a), None, 0, None) == L.OK
     for code in (0, -1, -2, -3, -4, -5, -6, -7, -8, -99):
         assert len(L.strerror(code)) > 5
     assert b"gfx950" in lib.moe_fp8_version()
+
+
+def test_packed_weight_entry_points(pkg, lib):
+    """The packed copy of W13 + W2 is exactly their size; missing or short buffers are reported
+    before anything is launched (also without a GPU)."""
+    L = pkg._lib
+    n = L.packed_weights_bytes()
+    assert n == 32 * 4096 * 7168 + 32 * 7168 * 2048 == 1_409_286_144
+    a = _args(pkg)
+    assert lib.moe_fp8_pack_weights(None, 0x1000, n, None) == L.EINVAL_POINTER
+    a.gemm2_weights = None
+    assert lib.moe_fp8_pack_weights(ctypes.byref(a), 0x1000, n, None) == L.EINVAL_POINTER
+    a = _args(pkg)
+    assert lib.moe_fp8_pack_weights(ctypes.byref(a), None, n, None) == L.EPACKED
+    assert lib.moe_fp8_pack_weights(ctypes.byref(a), 0x1000, n - 1, None) == L.EPACKED
+    big = L.workspace_bytes(4)
+    assert lib.moe_fp8_run_packed(ctypes.byref(a), None, n, 0x1000, big, None) == L.EPACKED
+    assert lib.moe_fp8_run_packed(ctypes.byref(a), 0x1000, n - 1, 0x1000, big, None) == L.EPACKED
+    # then the checks of moe_fp8_run
+    assert lib.moe_fp8_run_packed(ctypes.byref(a), 0x1000, n, 0x1000, big - 1, None) == L.EWORKSPACE
+    a.num_tokens = -1
+    assert lib.moe_fp8_run_packed(ctypes.byref(a), 0x1000, n, 0x1000, big, None) == L.EINVAL_TOKENS
+    assert len(L.strerror(L.EPACKED)) > 5
 
 
 def test_no_device_is_reported(pkg, lib):
