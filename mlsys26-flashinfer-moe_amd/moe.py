@@ -230,6 +230,12 @@ def packed_weights_for(gemm1_weights: torch.Tensor, gemm2_weights: torch.Tensor)
     return _packed_weights.get(gemm1_weights, gemm2_weights)
 
 
+def clear_packed_weights() -> None:
+    """Forgets run()'s packed copies (after writes to the weights that bypass torch); copies a
+    graph capture used stay alive."""
+    _packed_weights.clear()
+
+
 def set_packed_weight_sets(max_sets: int) -> None:
     """How many weight sets run() keeps a packed copy of (default 4, 1.41 GB each); 0 turns the
     packed path of run() off. Copies already built are kept (see PackedWeightCache.clear)."""
