@@ -180,8 +180,9 @@ int run_layer(const moe_fp8_args* args, void* workspace, size_t workspace_bytes,
   if (args->num_tokens == 0) return MOE_FP8_OK;
   const RouteParams rp = route_params(args, L, workspace, 0);
   GemmParams gp = gemm_params(args, L, workspace);
-  static_assert(MOE_FP8_PACKED_MAX_TOKENS == kFusedDispatchTokens, "the decode kernels read the packed copy");
-  const bool use_packed = packed && args->num_tokens <= MOE_FP8_PACKED_MAX_TOKENS;
+  // the streaming GEMMs (items of up to 32 rows) read the packed copy, the tile GEMMs do not
+  static_assert(MOE_FP8_PACKED_MAX_TOKENS == kStreamMaxTokens, "the streaming GEMMs' batches");
+  const bool use_packed = packed && L.rows_per_item <= 32;
   if (use_packed) {
     gp.w13 = packed;
     gp.w2 = packed + (packed_weights_bytes() - (size_t)kExpertsLocal * kHidden * kInter);
@@ -194,7 +195,7 @@ int run_layer(const moe_fp8_args* args, void* workspace, size_t workspace_bytes,
     if (launch_gemm1_dispatch(gp, rp, use_packed, stream) != hipSuccess || !mark(2)) return MOE_FP8_ELAUNCH;
   } else {
     if (launch_route_dispatch(rp, stream) != hipSuccess || !mark(1)) return MOE_FP8_ELAUNCH;
-    if (launch_gemm1(gp, L.rows_per_item, stream) != hipSuccess || !mark(2)) return MOE_FP8_ELAUNCH;
+    if (launch_gemm1(gp, L.rows_per_item, use_packed, stream) != hipSuccess || !mark(2)) return MOE_FP8_ELAUNCH;
   }
   if (launch_requant(gp, L.rows_per_item, stream) != hipSuccess) return MOE_FP8_ELAUNCH;
   if (launch_gemm2(gp, L.rows_per_item, use_packed, stream) != hipSuccess) return MOE_FP8_ELAUNCH;
@@ -271,7 +272,7 @@ int moe_fp8_gemm1(const moe_fp8_args* args, void* workspace, size_t workspace_by
   if (rc != MOE_FP8_OK) return rc;
   if (args->num_tokens == 0) return MOE_FP8_OK;
   const GemmParams p = gemm_params(args, L, workspace);
-  return launch_gemm1(p, L.rows_per_item, stream) == hipSuccess ? MOE_FP8_OK : MOE_FP8_ELAUNCH;
+  return launch_gemm1(p, L.rows_per_item, false, stream) == hipSuccess ? MOE_FP8_OK : MOE_FP8_ELAUNCH;
 }
 
 int moe_fp8_gemm2_combine(const moe_fp8_args* args, void* workspace, size_t workspace_bytes,

@@ -101,12 +101,11 @@ struct StreamStage {
 // readlane, so the loop holds no branches and the compiler's waits cover exactly the step
 // being consumed. Lane l ends with rows 4*(l/16)+i of each weight fragment against row
 // l%16 of each row group.
-// With PACKED (GEMM1 only) the weights come from the packed copy.
+// With PACKED the weights come from the packed copy.
 template <int KIND, int NG, bool PACKED = false>
 __device__ __forceinline__ void stream_accumulate(const GemmParams& p, int e, int r0, int rows, int slice,
                                                   int lane, const int32_t* row_token,
                                                   v4f (&acc)[StreamShape<KIND>::kFrags][NG]) {
-  static_assert(!PACKED || KIND == kG1, "packed weights: GEMM1 of the decode path");
   using S = StreamShape<KIND>;
   constexpr int KS = S::kSteps;
   constexpr int NF = S::kFrags;
@@ -131,15 +130,20 @@ __device__ __forceinline__ void stream_accumulate(const GemmParams& p, int e, in
   } else {
     const int row0 = slice * 16 * NF;                         // fragments at row0 + 16f
 #pragma unroll
-    for (int f = 0; f < NF; ++f)
-      wf[f] = p.w2 + ((size_t)e * kHidden + row0 + 16 * f + (lane & 15)) * kInter + (lane >> 4) * 16;
+    for (int f = 0; f < NF; ++f) {
+      if constexpr (PACKED)
+        wf[f] = p.w2 + (((size_t)e * (kHidden / 16) + row0 / 16 + f) * KS) * kPackedFrag + lane * 32;
+      else
+        wf[f] = p.w2 + ((size_t)e * kHidden + row0 + 16 * f + (lane & 15)) * kInter + (lane >> 4) * 16;
+    }
     const float sw = p.w2_scale[((size_t)e * kHBlocks + row0 / 128) * kIBlocks + (lane < KS ? lane : 0)];
 #pragma unroll
     for (int f = 0; f < NF; ++f) sw_lane[f] = sw;
   }
 
   // one K-step further along a weight fragment
-  constexpr size_t kWStep = PACKED ? 2 * kPackedFrag : 128;
+  // (packed W13 interleaves the gate and up fragments of a K-step)
+  constexpr size_t kWStep = PACKED ? (KIND == kG1 ? 2 : 1) * kPackedFrag : 128;
   auto wload = [&](const uint8_t* q) { return PACKED ? load_frag_packed(q) : load_frag(q); };
   StreamStage<NF, NG> ring[NB];
   // the weight loads of the first steps go out before the activation addresses are known
@@ -287,10 +291,11 @@ __device__ __forceinline__ void stream_units(const GemmParams& p, int n_items, c
   }
 }
 
-template <int KIND, int MAXNG>
+// PACKED: p.w13 / p.w2 is the packed copy (moe_fp8_run_packed).
+template <int KIND, int MAXNG, bool PACKED = false>
 __global__ __launch_bounds__(kStreamWaves * 64) void gemm_stream_kernel(GemmParams p) {
   const int n_items = min(p.counters[kCtrItems], p.max_items);
-  stream_units<KIND, MAXNG>(p, n_items, reinterpret_cast<const int4*>(p.work_items), p.sorted_token);
+  stream_units<KIND, MAXNG, PACKED>(p, n_items, reinterpret_cast<const int4*>(p.work_items), p.sorted_token);
 }
 
 // Columns per requantisation scale of 16-row items: the reference's 1x64 block
@@ -698,10 +703,10 @@ int resident_per_cu(K kernel, int& cache) {
 // One wave of resident work-groups: every work-group starts at once, and the round-robin
 // deal gives every CU the same number of units (a second, partial wave of work-groups
 // would run at a fraction of the occupancy).
-template <int KIND, int MAXNG>
+template <int KIND, int MAXNG, bool PACKED = false>
 hipError_t launch_stream_ng(const GemmParams& p, hipStream_t s) {
   static int occ = 0;
-  const auto kernel = gemm_stream_kernel<KIND, MAXNG>;
+  const auto kernel = gemm_stream_kernel<KIND, MAXNG, PACKED>;
   const int max_units = p.max_items * StreamShape<KIND>::kSlices;
   int grid = num_cus() * resident_per_cu(kernel, occ);
   const int cap = (max_units + kStreamWaves - 1) / kStreamWaves;
@@ -712,8 +717,9 @@ hipError_t launch_stream_ng(const GemmParams& p, hipStream_t s) {
 }
 
 template <int KIND>
-hipError_t launch_stream(const GemmParams& p, int rows_per_item, hipStream_t s) {
-  return rows_per_item <= 16 ? launch_stream_ng<KIND, 1>(p, s) : launch_stream_ng<KIND, 2>(p, s);
+hipError_t launch_stream(const GemmParams& p, int rows_per_item, bool packed, hipStream_t s) {
+  if (rows_per_item <= 16) return packed ? launch_stream_ng<KIND, 1, true>(p, s) : launch_stream_ng<KIND, 1>(p, s);
+  return packed ? launch_stream_ng<KIND, 2, true>(p, s) : launch_stream_ng<KIND, 2>(p, s);
 }
 
 // Writes the packed copy of W13 and W2: one 16-byte chunk per thread and iteration, in the
@@ -758,9 +764,9 @@ hipError_t launch_pack_weights(const uint8_t* w13, const uint8_t* w2, uint8_t* p
   return hipGetLastError();
 }
 
-hipError_t launch_gemm1(const GemmParams& p, int rows_per_item, hipStream_t s) {
+hipError_t launch_gemm1(const GemmParams& p, int rows_per_item, bool packed, hipStream_t s) {
   if (rows_per_item > 32) return launch_gemm1_tile(p, rows_per_item, s);
-  return launch_stream<kG1>(p, rows_per_item, s);
+  return launch_stream<kG1>(p, rows_per_item, packed, s);
 }
 
 hipError_t launch_gemm1_dispatch(const GemmParams& p, const RouteParams& rp, bool packed, hipStream_t s) {
@@ -797,7 +803,7 @@ hipError_t launch_gemm2(const GemmParams& p, int rows_per_item, bool packed, hip
     else hipLaunchKernelGGL(gemm2_slice_kernel<false>, dim3(kHiddenSlices), dim3(kSliceQuarters * 64), 0, s, p);
     return hipGetLastError();
   }
-  return launch_stream<kG2>(p, rows_per_item, s);
+  return launch_stream<kG2>(p, rows_per_item, packed, s);
 }
 
 hipError_t launch_combine(const GemmParams& p, int rows_per_item, hipStream_t s) {

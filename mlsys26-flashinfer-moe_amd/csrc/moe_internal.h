@@ -64,9 +64,13 @@ constexpr int kTileItemRowsLarge = 160;
 // 128 rows below 4096 tokens and up to 160 from there: larger items move fewer bytes per
 // flop, but at mid-size batches the fewer, longer units balance worse over the CUs (measured:
 // T=1024 GEMM1 170 us with 128-row items against 196 us with 160; T=8192 342 against 319).
+// Batches up to kStreamMaxTokens run the wavefront-granular streaming GEMMs (items of 16 or
+// 32 rows), larger ones the tile GEMMs.
+constexpr int kStreamMaxTokens = 512;
+
 inline int rows_per_item_for(int T) {
   if (T <= 64) return 16;
-  if (T <= 512) return 32;
+  if (T <= kStreamMaxTokens) return 32;
   if (T < 4096) return kTileItemRowsMid;
   return kTileItemRowsLarge;
 }
@@ -131,11 +135,12 @@ struct GemmParams {
 
 hipError_t launch_route_dispatch(const RouteParams& p, hipStream_t s);
 hipError_t launch_route(const RouteParams& p, hipStream_t s);
-hipError_t launch_gemm1(const GemmParams& p, int rows_per_item, hipStream_t s);
+// packed (items of up to 32 rows): p.w13 is the packed copy of W13 (moe_fp8_pack_weights).
+hipError_t launch_gemm1(const GemmParams& p, int rows_per_item, bool packed, hipStream_t s);
 // packed: p.w13 is the packed copy of W13 (moe_fp8_pack_weights).
 hipError_t launch_gemm1_dispatch(const GemmParams& p, const RouteParams& rp, bool packed, hipStream_t s);
 hipError_t launch_requant(const GemmParams& p, int rows_per_item, hipStream_t s);
-// packed (16-row items only): p.w2 is the packed copy of W2.
+// packed (items of up to 32 rows): p.w2 is the packed copy of W2.
 hipError_t launch_gemm2(const GemmParams& p, int rows_per_item, bool packed, hipStream_t s);
 // The packed copy of W13 and W2 read by the decode kernels (moe_fp8_pack_weights).
 size_t packed_weights_bytes();

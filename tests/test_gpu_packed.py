@@ -4,10 +4,11 @@
   here with numpy index arithmetic on the row-major weights (first and last blocks, blocks in
   the middle, both halves of a W13 block), and the whole copy as a permutation of the weights'
   bytes (equal byte sums and byte histograms of the W13 and W2 parts).
-* Results: run_packed is bit-identical to moe_fp8_run on the row-major weights up to 64 tokens,
-  where the decode GEMMs stream the packed copy (T = 1, 16, 64, another expert offset, fp32
-  output), and above 64 tokens, where the copy is not read (T = 100).
-* run() builds the copy of a weight set on its first call of up to 64 tokens, reuses it, gives
+* Results: run_packed is bit-identical to moe_fp8_run on the row-major weights up to 512 tokens,
+  where the streaming GEMMs read the packed copy (16-row items: T = 1, 16, 40, 64, other expert
+  offsets, fp32 output; 32-row items: T = 65, 300, 512), and above 512 tokens, where the copy
+  is not read (T = 600).
+* run() builds the copy of a weight set on its first call of up to 512 tokens, reuses it, gives
   the row-major result bit for bit, rebuilds it after an in-place change of the weights, and
   streams the row-major weights when the cache is off.
 """
@@ -81,7 +82,9 @@ def test_packed_copy_is_a_permutation_of_the_weights():
 
 @pytest.mark.parametrize("T,offset,out_dtype", [(1, 0, torch.bfloat16), (16, 0, torch.bfloat16),
                                                 (64, 0, torch.bfloat16), (64, 96, torch.bfloat16),
-                                                (40, 224, torch.float32), (100, 0, torch.bfloat16)])
+                                                (40, 224, torch.float32), (65, 0, torch.bfloat16),
+                                                (300, 32, torch.bfloat16), (512, 0, torch.float32),
+                                                (600, 0, torch.bfloat16)])
 def test_run_packed_is_bit_identical_to_run(T, offset, out_dtype):
     gh = _gh()
     dev = torch.device("cuda:0")
