@@ -4,9 +4,9 @@
 
 A step is one call of the layer (routing, dispatch, GEMM1+SwiGLU+requant, GEMM2+combine) over
 one batch of synthetic inputs already resident in HBM, through the C ABI as run() makes it: up
-to 512 tokens moe_fp8_run_packed with the packed copy of the weight set that run()'s cache keeps
+to 256 tokens moe_fp8_run_packed with the packed copy of the weight set that run()'s cache keeps
 (built on the set's first call, outside the timed region; row_major_us_per_step times
-moe_fp8_run on the row-major weights beside it), above 512 tokens moe_fp8_run. The headline
+moe_fp8_run on the row-major weights beside it), above 256 tokens moe_fp8_run. The headline
 workload is the 64-token decode batch (H=7168, I=2048, 32 local of 256 experts, top-8);
 `value` is its whole-layer algorithmic HBM throughput in GB/s:
     bytes = E_touched * 44,050,944 + T * 22,752 + 512
@@ -100,7 +100,7 @@ def workload_figures(T, n, e_touched, u, rows_per_item):
 
 def gemm1_kernel_name(T, rows_per_item, packed=False):
     """The one kernel of stage 2 (GEMM1) of the layer for a batch of T tokens (packed: the
-    packed copy of the weights, as run() streams it up to 512 tokens)."""
+    packed copy of the weights, as run() streams it up to 256 tokens)."""
     if T <= 64:
         return (("gemm1_stream_dispatch_kernel<true>", "gemm1_stream_dispatch_packed") if packed else
                 ("gemm1_stream_dispatch_kernel<false>", "gemm1_stream_dispatch"))
@@ -134,7 +134,7 @@ def bench_workload(pkg, inputs, name, weight_sets, steps, warmup):
                                  inputs.ROUTED_SCALING_FACTOR, out))
     nbytes = ws.buffer.numel()
     R = len(argsets)
-    # Up to 512 tokens run() streams a packed copy of each weight set, which its cache builds on
+    # Up to 256 tokens run() streams a packed copy of each weight set, which its cache builds on
     # the first call with the set (outside every timed region here); the C-ABI steps do the same.
     packs = None
     if T <= _lib.PACKED_MAX_TOKENS:
@@ -257,7 +257,7 @@ def bench_workload(pkg, inputs, name, weight_sets, steps, warmup):
                              requant_gemm2_combine=round(stage_ms[2] * 1e3, 2)))
     res["rows_per_item"] = rpi
     if packs is not None:
-        res["weights"] = "packed copy per weight set (as run() streams up to 512 tokens)"
+        res["weights"] = "packed copy per weight set (as run() streams up to 256 tokens)"
         res["row_major_us_per_step"] = round(row_major_ms * 1e3, 2)
     res["hbm_roofline_frac"] = round(res["hbm_gbs"] / HBM_PEAK_GBS, 4)
     res["mfma_roofline_frac"] = round(res["tflops"] / FP8_PEAK_TFLOPS, 4)

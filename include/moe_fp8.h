@@ -124,7 +124,7 @@ typedef struct moe_fp8_args {
  *                                        bytes up to 64: the combine happens inside GEMM2)
  *                                                                                     (kernel.py:704)
  *   swiglu        fp32  [N_max, 2048]    SwiGLU output before requantisation; only for
- *                                        T <= 512 (0 bytes otherwise)
+ *                                        T <= 256 (0 bytes otherwise)
  */
 typedef struct moe_fp8_layout {
   size_t total_bytes;
@@ -188,7 +188,7 @@ int moe_fp8_run_profiled(const moe_fp8_args* args, const void* packed, size_t pa
 
 /* A cached re-layout of the expert weights for the decode path, behind the same tensor
  * contract: the caller keeps passing W13/W2 in their kernel.py:604-607 layout and may, once per
- * weight set, build a packed copy that the streaming GEMMs of batches up to 512 tokens read
+ * weight set, build a packed copy that the streaming GEMMs of batches up to 256 tokens read
  * instead.
  * In the copy each wavefront's MFMA operand for a 128-wide K-step is contiguous (32 bytes per
  * lane, 2 KB per 16-row fragment): W13 as blocks [expert][16 SwiGLU columns][K-step] of 4 KB
@@ -197,15 +197,15 @@ int moe_fp8_run_profiled(const moe_fp8_args* args, const void* packed, size_t pa
  * [64 + 16(l/16), +16) of the block's row l%16. Scales are not copied. An extension
  * of the path with no counterpart in the reference, whose kernels read the weights row-major
  * (kernel.py:91-102, 222-226). */
-#define MOE_FP8_PACKED_MAX_TOKENS 512         /* the largest batch that reads the packed copy */
+#define MOE_FP8_PACKED_MAX_TOKENS 256         /* the largest batch that reads the packed copy */
 size_t moe_fp8_packed_weights_bytes(void);   /* 1,409,286,144: the size of W13 plus W2 */
 
 /* Writes the packed copy of args->gemm1_weights and args->gemm2_weights (only those two fields
  * are read) into `packed` on `stream`. */
 int moe_fp8_pack_weights(const moe_fp8_args* args, void* packed, size_t packed_bytes, hipStream_t stream);
 
-/* moe_fp8_run with the packed copy of args' weights: up to 512 tokens GEMM1 and GEMM2 stream
- * `packed` instead of args->gemm1_weights / gemm2_weights; above 512 tokens `packed` is not
+/* moe_fp8_run with the packed copy of args' weights: up to 256 tokens GEMM1 and GEMM2 stream
+ * `packed` instead of args->gemm1_weights / gemm2_weights; above 256 tokens `packed` is not
  * read. The output is bit-identical to moe_fp8_run's (the same arithmetic in the same order).
  * Replaces run() (kernel.py:562-729) like moe_fp8_run. */
 int moe_fp8_run_packed(const moe_fp8_args* args, const void* packed, size_t packed_bytes, void* workspace,

@@ -66,7 +66,7 @@ constexpr int kTileItemRowsLarge = 160;
 // T=1024 GEMM1 170 us with 128-row items against 196 us with 160; T=8192 342 against 319).
 // Batches up to kStreamMaxTokens run the wavefront-granular streaming GEMMs (items of 16 or
 // 32 rows), larger ones the tile GEMMs.
-constexpr int kStreamMaxTokens = 512;
+constexpr int kStreamMaxTokens = 256;
 
 inline int rows_per_item_for(int T) {
   if (T <= 64) return 16;

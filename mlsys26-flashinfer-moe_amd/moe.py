@@ -147,10 +147,10 @@ def workspace_for(num_tokens: int, device: torch.device) -> Workspace:
 
 
 class PackedWeightCache:
-    """Packed copies of weight sets (pack_weights) that run() streams up to 512 tokens.
+    """Packed copies of weight sets (pack_weights) that run() streams up to 256 tokens.
 
     The weights keep their kernel.py:604-607 contract: run() receives them row-major as ever,
-    and the first call of up to 512 tokens with a weight set builds its packed copy (one kernel
+    and the first call of up to 256 tokens with a weight set builds its packed copy (one kernel
     on the current stream, 1.41 GB), which later calls with the same set stream instead. A copy
     belongs to the weights' storage (W13's and W2's device addresses, held by weak reference) and
     to their version counters: modifying the weights in place through torch, or freeing them and
@@ -286,7 +286,7 @@ def run(
     `output` [T, 7168]. A bf16 or fp32 `output` on the GPU is written directly by the
     kernels; any other dtype or device receives a copy_ of a bf16 result.
 
-    Up to 512 tokens, with contiguous weights already on the GPU, the GEMMs stream a packed copy
+    Up to 256 tokens, with contiguous weights already on the GPU, the GEMMs stream a packed copy
     of the weight set that the first such call builds and later calls reuse (PackedWeightCache;
     set_packed_weight_sets(0) turns it off). The output is bit-identical either way.
     """
@@ -327,7 +327,7 @@ def pack_weights(gemm1_weights: torch.Tensor, gemm2_weights: torch.Tensor) -> to
 def run_packed(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
                gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, local_expert_offset: int,
                routed_scaling_factor: float, output: torch.Tensor, *, packed_weights: torch.Tensor):
-    """run() with the packed copy of this weight set (pack_weights): up to 512 tokens the GEMMs
+    """run() with the packed copy of this weight set (pack_weights): up to 256 tokens the GEMMs
     stream `packed_weights` instead of gemm1_weights / gemm2_weights; the output is bit-identical
     to run()'s."""
     assert packed_weights.dtype == torch.uint8 and packed_weights.is_contiguous() and \

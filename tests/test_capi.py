@@ -53,7 +53,7 @@ def test_layout_consistent(pkg, T):
     # up to 64 tokens (16-row items) the requantisation is per 64 columns and GEMM2 combines in
     # LDS (no parked rows); items of up to 32 rows keep GEMM1's fp32 SwiGLU rows
     decode = L.rows_per_item == 16
-    assert L.rows_per_item == (16 if T <= 64 else 32 if T <= 512 else L.rows_per_item)
+    assert L.rows_per_item == (16 if T <= 64 else 32 if T <= 256 else L.rows_per_item)
     assert L.requant_block == (64 if decode else 128)
     arrays = [
         ("topk_ids", 4 * 8 * T), ("topk_weights", 4 * 8 * T), ("expert_count", 4 * 32),

@@ -339,8 +339,8 @@ def _given_topk(case, T, rng):
     return ids, w
 
 
-@pytest.mark.parametrize("T,case", [(1, "all_local"), (40, "repeat"), (64, "all_local"), (65, "repeat"), (300, "all_local"),
-                                    (513, "all_local"), (600, "one_expert"), (600, "none_local"),
+@pytest.mark.parametrize("T,case", [(1, "all_local"), (40, "repeat"), (64, "all_local"), (65, "repeat"), (256, "all_local"),
+                                    (257, "all_local"), (600, "one_expert"), (600, "none_local"),
                                     (4095, "all_local"), (4096, "all_local"), (4100, "few_local")])
 def test_layer_edge_cases_given_topk(T, case):
     """The GEMM stages on constructed top-k lists: one token, a repeated expert, every token
@@ -348,7 +348,7 @@ def test_layer_edge_cases_given_topk(T, case):
     16-row-item batch with every slot local (T=64: 512 rows, up to 64 items) and the first
     32-row-item batch (T=65), and at T >= 4096
     (items of up to 160 rows) items of every shape next to thousands of tokens without a
-    local expert. T=513 is the first batch on the tile kernels; T=4095 and T=4096 put 1024 rows
+    local expert. T=257 is the first batch on the tile kernels; T=4095 and T=4096 put 1024 rows
     on every local expert, the largest batch of 128-row items and the first of 160-row items."""
     gh = _gh()
     dev = torch.device("cuda:0")

@@ -4,11 +4,11 @@
   here with numpy index arithmetic on the row-major weights (first and last blocks, blocks in
   the middle, both halves of a W13 block), and the whole copy as a permutation of the weights'
   bytes (equal byte sums and byte histograms of the W13 and W2 parts).
-* Results: run_packed is bit-identical to moe_fp8_run on the row-major weights up to 512 tokens,
+* Results: run_packed is bit-identical to moe_fp8_run on the row-major weights up to 256 tokens,
   where the streaming GEMMs read the packed copy (16-row items: T = 1, 16, 40, 64, other expert
-  offsets, fp32 output; 32-row items: T = 65, 300, 512), and above 512 tokens, where the copy
-  is not read (T = 600).
-* run() builds the copy of a weight set on its first call of up to 512 tokens, reuses it, gives
+  offsets, fp32 output; 32-row items: T = 65, 200, 256), and above 256 tokens, where the copy
+  is not read (T = 257, 600).
+* run() builds the copy of a weight set on its first call of up to 256 tokens, reuses it, gives
   the row-major result bit for bit, rebuilds it after an in-place change of the weights, and
   streams the row-major weights when the cache is off.
 """
@@ -83,7 +83,7 @@ def test_packed_copy_is_a_permutation_of_the_weights():
 @pytest.mark.parametrize("T,offset,out_dtype", [(1, 0, torch.bfloat16), (16, 0, torch.bfloat16),
                                                 (64, 0, torch.bfloat16), (64, 96, torch.bfloat16),
                                                 (40, 224, torch.float32), (65, 0, torch.bfloat16),
-                                                (300, 32, torch.bfloat16), (512, 0, torch.float32),
+                                                (200, 32, torch.bfloat16), (256, 0, torch.float32), (257, 0, torch.bfloat16),
                                                 (600, 0, torch.bfloat16)])
 def test_run_packed_is_bit_identical_to_run(T, offset, out_dtype):
     gh = _gh()
