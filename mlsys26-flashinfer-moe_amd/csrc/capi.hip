@@ -155,6 +155,14 @@ int compute_layout(int32_t T, moe_fp8_layout* out) {
   L.partial = take(rpi == 16 ? 0 : t * kTopK * kHidden * sizeof(float));
   L.swiglu = take(rpi <= 32 ? nmax * kInter * sizeof(float) : 0);
   L.total_bytes = off;
+  // The streaming batches' largest workspace (with its fp32 SwiGLU rows) exceeds the first tile
+  // batches' own: every tile batch reserves at least that much, so that the size is
+  // non-decreasing in T and a workspace sized for T_max serves every T <= T_max.
+  if (T > kStreamMaxTokens) {
+    moe_fp8_layout S;
+    compute_layout(kStreamMaxTokens, &S);
+    if (S.total_bytes > L.total_bytes) L.total_bytes = S.total_bytes;
+  }
   L.num_tokens = T;
   L.max_assignments = (int32_t)nmax;
   L.max_work_items = max_items;

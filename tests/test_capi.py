@@ -73,6 +73,15 @@ def test_layout_consistent(pkg, T):
     assert pkg._lib.workspace_bytes(T) == L.total_bytes
 
 
+def test_workspace_size_is_non_decreasing(pkg):
+    """A workspace sized for T_max serves every T <= T_max, across the regime boundaries (16-row
+    items up to 64 tokens, 32-row items up to 256, 128-row tiles below 4096, 160-row above)."""
+    L = pkg._lib
+    Ts = list(range(0, 70)) + list(range(250, 262)) + list(range(4088, 4100)) + [8192, 32768]
+    sizes = [L.workspace_bytes(T) for T in Ts]
+    assert all(a <= b for a, b in zip(sizes, sizes[1:])), [(T, s) for T, s in zip(Ts, sizes)]
+
+
 def test_invalid_tokens(pkg, lib):
     assert lib.moe_fp8_workspace_bytes(-1) == 0
     assert lib.moe_fp8_workspace_bytes((1 << 20) + 1) == 0
