@@ -422,6 +422,30 @@ def test_layer_last_expert_group():
     assert rel <= 0.01, f"offset 224 vs emulated oracle: rel rms {rel:.4g}"
 
 
+def test_one_workspace_across_the_streaming_tile_boundary():
+    """A workspace sized for T_max (here the first tile batch, 300 tokens) serves smaller batches
+    on the streaming GEMMs, whose fp32 SwiGLU rows need more room than the tile batch's own
+    arrays: 256, 300 and 64 tokens on one workspace give the same output as fresh workspaces."""
+    gh = _gh()
+    dev = torch.device("cuda:0")
+    w, _ = _weights()
+    shared = gh.new_workspace(300, dev)
+    for T in (256, 300, 64):
+        print(f"shared workspace T={T}", flush=True)
+        logits, bias, hq, hs = gh.inputs.make_activations(T, 8800 + T, dev)
+        kw = dict(routing_logits=logits, routing_bias=bias, hidden_states=hq, hidden_states_scale=hs,
+                  gemm1_weights=w[0], gemm1_weights_scale=w[1], gemm2_weights=w[2], gemm2_weights_scale=w[3],
+                  local_expert_offset=0, routed_scaling_factor=2.5)
+        a = torch.full((T, 7168), float("nan"), dtype=torch.bfloat16, device=dev)
+        b = torch.full((T, 7168), float("nan"), dtype=torch.bfloat16, device=dev)
+        shared.layout = gh._lib.workspace_layout(T)
+        gh.run_layer(gh.make_args(**kw, output=a), shared)
+        gh.run_layer(gh.make_args(**kw, output=b), gh.new_workspace(T, dev))
+        torch.cuda.synchronize()
+        assert torch.isfinite(a.float()).all()
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
 def test_zero_tokens():
     gh = _gh()
     dev = torch.device("cuda:0")
