@@ -4,11 +4,11 @@
 //   caller tensors   : the contract of kernel.py:591-607 (see include/moe_fp8.h)
 //   workspace arrays : moe_fp8_layout offsets; every array is 256-byte aligned.
 // Kernels of one call run in this order on one stream:
-//   T <= 64 (moe_fp8_run): route_kernel<false> -> gemm1_stream_dispatch_kernel (GEMM1 that
+//   T <= 64 (moe_fp8_run): route_wide_kernel -> gemm1_stream_dispatch_kernel (GEMM1 that
 //   rebuilds the dispatch itself) -> requant_kernel -> gemm2_slice_kernel (GEMM2 and the
 //   combine); otherwise
-//   route_dispatch_small_kernel | (route_kernel<false> -> dispatch_small_kernel)
-//   | (route_kernel<true> -> scan_kernel -> place_kernel)
+//   (route_wide_kernel (T <= 64) | route_kernel<false>) -> dispatch_small_kernel
+//   | (route_kernel<true> -> place_kernel)
 //   -> GEMM1 -> [requant_kernel] -> GEMM2 -> [combine_kernel]
 // where, with <= 32 rows per work item, GEMM1 is gemm_stream_kernel<1> and leaves fp32 SwiGLU
 // rows for requant_kernel, and GEMM2 is gemm2_slice_kernel (16-row items, up to 64 tokens)
@@ -35,8 +35,10 @@ constexpr int kBlock = MOE_FP8_BLOCK;          // 128
 constexpr int kHBlocks = MOE_FP8_H_BLOCKS;     // 56
 constexpr int kIBlocks = MOE_FP8_I_BLOCKS;     // 16
 
-// Routing: 16 lanes per token, 16 tokens per work-group of 4 wavefronts; the one-work-group
-// dispatch of small batches and the scan use 1024 threads.
+// Routing: up to kWideRouteTokens tokens one token per wavefront (4 per work-group), above
+// that 16 lanes per token and 16 tokens per work-group of 4 wavefronts; the one-work-group
+// dispatch of small batches uses 1024 threads.
+constexpr int kWideRouteTokens = 64;
 constexpr int kRouteTokensPerBlock = 16;
 constexpr int kRouteThreads = 1024;
 // Up to this many tokens routing and dispatch run in a single work-group (one launch).

@@ -1,13 +1,14 @@
 // Routing and dispatch for the fused MoE layer (gfx950).
 //
-// Sixteen lanes per token (four tokens per wavefront) compute the DeepSeek-V3 no-aux grouped
-// routing (kernel.py:428-542) with branch-free DPP reductions inside 16-lane rows. Dispatch
-// then histograms the local assignments, scans them into CSR offsets, builds the GEMM work
-// list and places every assignment in its bucket:
-//   T <= 16:  route_dispatch_small_kernel, one work-group that routes and then dispatches
-//             in LDS (one launch);
+// The DeepSeek-V3 no-aux grouped routing (kernel.py:428-542) runs with branch-free DPP
+// reductions: up to 64 tokens one token per wavefront (route_wide_kernel: 4 experts per lane,
+// the shortest dependent chain per token), above that sixteen lanes per token and four
+// tokens per wavefront (route_kernel). Dispatch then histograms the local assignments, scans
+// them into CSR offsets, builds the GEMM work list and places every assignment in its bucket:
+//   T <= 64:  route_wide_kernel -> dispatch_small_kernel, which does the whole dispatch in one
+//             work-group, in LDS (moe_fp8_run rebuilds the dispatch inside GEMM1 instead);
 //   T <= 256 (or given top-k lists): route_kernel<false> (16 tokens per work-group) ->
-//             dispatch_small_kernel, which does the whole dispatch in one work-group, in LDS;
+//             dispatch_small_kernel;
 //   larger T: route_kernel<true> (also per work-group histograms and ranks) -> place_kernel
 //             (each work-group reduces the histograms it needs). No kernel synchronises
 //             across work-groups.
@@ -192,6 +193,93 @@ __device__ __forceinline__ int route_wave(const RouteParams& p, const float* s_b
   return r < kTopK ? my_id : -1;
 }
 
+// DPP row broadcasts across the 16-lane rows of a wavefront (GFX9): lane 15 of each row to
+// the next row (rows 1 and 3 take it), lane 31 to rows 2 and 3.
+constexpr int kDppRowBcast15 = 0x142;
+constexpr int kDppRowBcast31 = 0x143;
+
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ uint64_t dpp_u64_rows(uint64_t v) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)v, CTRL, ROW_MASK, 0xF, false);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(v >> 32), CTRL, ROW_MASK, 0xF, false);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+// Routing of token t by one wavefront (kernel.py:428-542), for small batches: lane l holds
+// experts 4l..4l+3, so group g (32 experts) is lanes 8g..8g+7, and every lane does a quarter
+// of route_wave's per-token work. The selections are route_wave's: the same argmax keys, the
+// group score as the sum of the group's two largest biased scores, the kept groups by (score,
+// lower index), the weights summed in selection order with the same fp32 operations, so
+// the top-k lists are bit-identical. `lg` holds the lane's four logits. Returns in lanes
+// k < 8 the expert of top-k slot k and its weight; other lanes return -1.
+__device__ __forceinline__ int route_wide(const RouteParams& p, const float* s_bias, int t, const float4 lg,
+                                          float& w_out) {
+  const int lane = lane_id();
+  const float4 cb = reinterpret_cast<const float4*>(s_bias)[lane];
+  const float xs[4] = {lg.x, lg.y, lg.z, lg.w}, cs[4] = {cb.x, cb.y, cb.z, cb.w};
+  float b[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) b[j] = sigmoid_f32(xs[j]) + cs[j];   // kernel.py:466-467
+  // group score (kernel.py:479-488): top-2 of the lane's four, then of the group's 8 lanes
+  float m1 = fmaxf(b[0], b[1]), m2 = fminf(b[0], b[1]);
+#pragma unroll
+  for (int i = 2; i < 4; ++i) {
+    const float n2 = __builtin_amdgcn_fmed3f(m1, m2, b[i]);
+    m1 = fmaxf(m1, b[i]);
+    m2 = n2;
+  }
+  top2_merge(m1, m2, dpp_f32<kDppXor1>(m1), dpp_f32<kDppXor1>(m2));
+  top2_merge(m1, m2, dpp_f32<kDppXor2>(m1), dpp_f32<kDppXor2>(m2));
+  top2_merge(m1, m2, dpp_f32<kDppHalfMirror>(m1), dpp_f32<kDppHalfMirror>(m2));
+  const float gs = m1 + m2;
+  // the 4 best groups (kernel.py:495-501): the eight scores are wave-uniform (lane 8h holds
+  // group h's), and a group is kept iff fewer than 4 groups rank before it
+  const int g = lane >> 3;
+  int rank = 0;
+#pragma unroll
+  for (int h = 0; h < kNGroup; ++h) {
+    const float hs = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(gs), 8 * h));
+    rank += (hs > gs || (hs == gs && h < g)) ? 1 : 0;
+  }
+  const bool kept = rank < kTopKGroup;
+  // top-8 experts of the kept groups (kernel.py:515-534): 8 rounds of (argmax inside the
+  // lane, argmax of the 64-bit keys across the wavefront, removal of the winner)
+  uint32_t c[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) c[i] = kept ? ordered(b[i]) : kOrderedNegInf;
+  const uint32_t lo_base = 0xFFFFu - 4u * (uint32_t)lane;
+  int my_id = -1;
+#pragma unroll
+  for (int k = 0; k < kTopK; ++k) {
+    const bool h01 = c[1] > c[0], h23 = c[3] > c[2];
+    const uint32_t v01 = h01 ? c[1] : c[0], v23 = h23 ? c[3] : c[2];
+    const uint32_t i01 = h01 ? 1u : 0u, i23 = h23 ? 3u : 2u;
+    const bool hi = v23 > v01;
+    uint64_t key = ((uint64_t)(hi ? v23 : v01) << 32) | (lo_base - (hi ? i23 : i01));
+    key = max_u64(key, dpp_u64<kDppXor1>(key));
+    key = max_u64(key, dpp_u64<kDppXor2>(key));
+    key = max_u64(key, dpp_u64<kDppHalfMirror>(key));
+    key = max_u64(key, dpp_u64<kDppMirror>(key));
+    key = max_u64(key, dpp_u64_rows<kDppRowBcast15, 0xA>(key));
+    key = max_u64(key, dpp_u64_rows<kDppRowBcast31, 0xC>(key));
+    // lane 63 holds the wavefront's largest key
+    const uint32_t klo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)key, 63);
+    const int e = key_index((uint64_t)klo);
+    my_id = (lane == k) ? e : my_id;
+    const uint32_t drop = ((e >> 2) == lane) ? (uint32_t)(e & 3) : 4u;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) c[i] = (drop == (uint32_t)i) ? 0u : c[i];
+  }
+  // weights (kernel.py:537-538), as route_wave: w = s / (s_0 + ... + s_7 + 1e-20) * rsf
+  const float sv = (lane < kTopK) ? sigmoid_f32(p.logits[(size_t)t * kExpertsGlobal + my_id]) : 0.0f;
+  float sum = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sv), 0));
+#pragma unroll
+  for (int k = 1; k < kTopK; ++k) sum = sum + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sv), k));
+  sum = sum + 1e-20f;
+  w_out = __fdiv_rn(sv, sum) * p.rsf;
+  return lane < kTopK ? my_id : -1;
+}
+
 __device__ __forceinline__ int local_of(int id, int offset) {
   const int le = id - offset;
   return (le >= 0 && le < kExpertsLocal) ? le : -1;
@@ -358,47 +446,21 @@ __device__ __forceinline__ void dispatch_slots(const RouteParams& p, int le, flo
   }
 }
 
-// Routing and dispatch of up to 64 tokens in one work-group of 16 wavefronts (one launch
-// instead of two dependent ones): wavefront w routes tokens 4w..4w+3, and the top-k lists
-// reach the one-slot-per-thread dispatch through LDS (they are also written to the
-// workspace, which the combine reads). Used up to kFusedRouteTokens tokens: routing is
-// VALU-heavy, and more than one routing wavefront per SIMD on one CU costs more than the
-// saved launch (T=16: 12.1 us against 14.0 us for the two kernels; T=64: 18.8 us against
-// 13.9 us).
-constexpr int kFusedRouteTokens = 16;
-constexpr int kFusedMaxTokens = kRouteThreads / 64 * 4;   // 64: four tokens per wavefront
-static_assert(kFusedRouteTokens <= kFusedMaxTokens, "one routing round");
-
-__global__ __launch_bounds__(kRouteThreads) void route_dispatch_small_kernel(RouteParams p) {
+// Routing of up to kWideRouteTokens tokens, one token per wavefront and four per work-group
+// (route_wide): top-k lists only, the dispatch follows in its own kernel or in GEMM1.
+__global__ __launch_bounds__(256) void route_wide_kernel(RouteParams p) {
   __shared__ __attribute__((aligned(16))) float s_bias[kExpertsGlobal];
-  __shared__ int s_id[kFusedMaxTokens * kTopK];
-  __shared__ float s_wt[kFusedMaxTokens * kTopK];
-  __shared__ int s_wcnt[16][kExpertsLocal];
-  __shared__ int s_cnt[kExpertsLocal];
-  __shared__ int s_start[kExpertsLocal + 1];
-  const int tid = threadIdx.x;
   const int lane = lane_id();
-  const int r = lane & 15;
-  const int tw = (tid >> 6) * 4;   // first token of the wavefront (uniform)
-  float4 lg[4];
-  if (tw < p.T) load_logits(p, tw, lg);
+  const int tw = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int t = min(tw, p.T - 1);   // wavefronts past the end recompute the last token
+  const float4 lg = reinterpret_cast<const float4*>(p.logits + (size_t)t * kExpertsGlobal)[lane];
   stage_bias(p, s_bias);
-  if (tw < p.T) {
-    float w = 0.f;
-    const int id = route_wave(p, s_bias, tw, lg, w);
-    const int t = tw + (lane >> 4);
-    if (t < p.T && r < kTopK) {
-      s_id[t * kTopK + r] = id;
-      s_wt[t * kTopK + r] = w;
-      p.topk_ids[t * kTopK + r] = id;
-      p.topk_w[t * kTopK + r] = w;
-    }
+  float w = 0.f;
+  const int id = route_wide(p, s_bias, t, lg, w);
+  if (tw < p.T && lane < kTopK) {
+    p.topk_ids[t * kTopK + lane] = id;
+    p.topk_w[t * kTopK + lane] = w;
   }
-  __syncthreads();
-  const int nslots = p.T * kTopK;
-  const int le = tid < nslots ? local_of(s_id[tid], p.offset) : -1;
-  const float w = tid < nslots ? s_wt[tid] : 0.f;
-  dispatch_slots(p, le, w, nslots, s_wcnt, s_cnt, s_start);
 }
 
 // Dispatch of small batches (T <= kSinglePassTokens) in one work-group, from the top-k
@@ -528,17 +590,20 @@ __global__ __launch_bounds__(kPlaceThreads) void place_kernel(RouteParams p) {
   p.sorted_slot[pos] = s;
 }
 
-hipError_t launch_route(const RouteParams& p, hipStream_t s) {
-  hipLaunchKernelGGL(route_kernel<false>, dim3(p.nblocks), dim3(kRouteWaves * 64), 0, s, p);
+// top-k lists only (no dispatch)
+static hipError_t launch_route_lists(const RouteParams& p, hipStream_t s) {
+  if (p.T <= kWideRouteTokens)
+    hipLaunchKernelGGL(route_wide_kernel, dim3((p.T + 3) / 4), dim3(256), 0, s, p);
+  else
+    hipLaunchKernelGGL(route_kernel<false>, dim3(p.nblocks), dim3(kRouteWaves * 64), 0, s, p);
   return hipGetLastError();
 }
 
+hipError_t launch_route(const RouteParams& p, hipStream_t s) { return launch_route_lists(p, s); }
+
 hipError_t launch_route_dispatch(const RouteParams& p, hipStream_t s) {
-  if (p.single_pass && !p.skip_routing && p.T <= kFusedRouteTokens) {
-    hipLaunchKernelGGL(route_dispatch_small_kernel, dim3(1), dim3(kRouteThreads), 0, s, p);
-  } else if (p.single_pass) {
-    if (!p.skip_routing)
-      hipLaunchKernelGGL(route_kernel<false>, dim3(p.nblocks), dim3(kRouteWaves * 64), 0, s, p);
+  if (p.single_pass) {
+    if (!p.skip_routing && launch_route_lists(p, s) != hipSuccess) return hipGetLastError();
     hipLaunchKernelGGL(dispatch_small_kernel, dim3(1), dim3(kRouteThreads), 0, s, p);
   } else {
     hipLaunchKernelGGL(route_kernel<true>, dim3(p.nblocks), dim3(kRouteWaves * 64), 0, s, p);

@@ -1,5 +1,9 @@
 """GPU parity of routing + dispatch (moe_fp8_route_dispatch) against the oracle.
 
+Up to 64 tokens a wavefront routes one token (route_wide_kernel, the routing moe_fp8_run uses
+at those sizes); above, sixteen lanes route one token (route_kernel). Both are checked on the
+golden router logits, every bias dtype, ties and extreme values.
+
 Bar: bit-exact. Expert ids, routing weights (as fp32 bit patterns), histogram, CSR
 offsets, the stable bucket permutation, per-token local counts and the GEMM work list
 must equal the oracle's exactly.
@@ -51,10 +55,27 @@ def test_routing_bit_exact_on_golden_logits(part):
     gh.check_dispatch(ws, rid, rw, 0, T)
 
 
+@pytest.mark.parametrize("part", [0, 1, 2])
+def test_routing_bit_exact_on_golden_logits_small_batches(part):
+    """Up to 64 tokens a wavefront routes one token (route_wide_kernel): the golden rows of each
+    bias set in batches of 64 and of 1."""
+    m = GOLD["bias_index"] == part
+    logits_all, bias = GOLD["logits"][m], GOLD["bias_sets"][part]
+    for lo in range(0, logits_all.shape[0], 64):
+        logits = logits_all[lo:lo + 64]
+        for batch in ((logits,) if lo else (logits, logits[:1])):
+            ws, gh = _route_gpu(batch, bias)
+            T = batch.shape[0]
+            rid, rw = orouting.route(batch, bias, 2.5)
+            assert np.array_equal(gh.read(ws, "topk_ids", torch.int32, T * 8).reshape(T, 8), rid)
+            assert np.array_equal(gh.read(ws, "topk_weights", torch.float32, T * 8).reshape(T, 8).view(np.uint32),
+                                  rw.view(np.uint32))
+
+
+@pytest.mark.parametrize("T", [40, 77])
 @pytest.mark.parametrize("bias_dtype", [torch.float32, torch.bfloat16, torch.float16])
-def test_routing_bias_dtypes(bias_dtype):
+def test_routing_bias_dtypes(bias_dtype, T):
     rng = np.random.default_rng(21)
-    T = 77
     logits = rng.standard_normal((T, 256)).astype(np.float32)
     bias = (rng.standard_normal(256) * 0.1).astype(np.float32)
     ws, gh = _route_gpu(logits, bias, bias_dtype=bias_dtype)
