@@ -456,26 +456,35 @@ __global__ __launch_bounds__(256) void requant_kernel(GemmParams p) {
 }
 
 // Decode batches of up to kFusedDispatchTokens tokens (16-row items): GEMM2 and the combine in
-// one kernel, with no fp32 rows parked in `partial`. A work-group owns 32 hidden rows of W2
-// (two MFMA fragments; 224 slices) across every work item, and its wavefront q owns K-steps
+// one kernel, with no fp32 rows parked in `partial`. A work-group owns 28 hidden rows of W2
+// (256 slices, one per CU: two MFMA fragments, the second's last four rows repeating its last
+// row and never stored) across every work item, and its wavefront q owns K-steps
 // [4q, 4q+4) of each: per item, q streams the expert's 32 x 512 weight bytes and the item's
 // act rows through a register ring, scales each 128-wide block product (kernel.py:234),
 // weights it by the routing weight (kernel.py:236-237) and adds it into its own LDS
 // accumulator of (token, hidden row). Items come in expert order, so each token's
 // contributions are added in ascending local expert order, and the rows of one token inside
 // an item (a repeated expert id) in slot order; the work-group then sums its four K quarters
-// in fixed order and writes the 32 columns of every token, zeros for tokens without a local
+// in fixed order and writes the 28 columns of every token, zeros for tokens without a local
 // expert (the zero-fill and finalize of kernel.py:704, 729). Deterministic, no atomics.
+// 28-row slices against 32-row ones (224 work-groups, 32 CUs idle): every output element is
+// computed by the same operations in the same order, and the weight stream spreads over all
+// 256 CUs.
 // Slice width, measured at T=64 / T=16 (GEMM2 with the requantisation before it, us): one
 // fragment 78.0 / 39.8, two 63.9 / 33.7, four 101.6 / 52.6, against 68.0 / 40.0 for the
 // wavefront-per-unit GEMM2 plus combine_kernel. One fragment spends a 2 KB activation
 // fragment and four small loads on every 2 KB of weights; four need more registers than two
 // wavefronts per SIMD allow, and one wavefront per SIMD cannot keep the matrix core busy.
 constexpr int kSliceF = 2;                               // weight fragments per wavefront
+constexpr int kSliceRows = 28;                           // hidden rows per work-group
 constexpr int kSliceQuarters = 4;                        // wavefronts per work-group = K quarters
 constexpr int kSliceSteps = kIBlocks / kSliceQuarters;   // 4 K-steps per quarter and item
 constexpr int kSliceRing = kSliceSteps;                  // ring slots: 3 steps in flight
-constexpr int kHiddenSlices = kHidden / (16 * kSliceF);  // 224
+constexpr int kHiddenSlices = kHidden / kSliceRows;      // 256
+static_assert(kHidden % kSliceRows == 0 && kSliceRows > 16 * (kSliceF - 1) && kSliceRows <= 16 * kSliceF,
+              "slice rows");
+// a lane's four output rows of a fragment are 4-aligned, so they share one 128-row W2 scale block
+static_assert(kSliceRows % 4 == 0 && kBlock % 4 == 0, "scale blocks");
 static_assert(kSliceRing == kSliceSteps, "one ring turn per item: slot u is K-step u of the item");
 static_assert(kFusedItems <= 64, "one work item per lane");
 
@@ -483,7 +492,7 @@ struct SliceStage {
   v8i w[kSliceF];   // W2 fragments: the slice's hidden rows 16f.. x 128 K bytes
   v8i a;            // act fragment: the item's 16 rows (rows past its end repeat its first row)
   float2 sa;        // act scales of the lane's row for the two 64-column halves of the K block
-  float sw;         // W2 block scale (the same for every lane)
+  float sw[kSliceF];  // W2 block scale of the lane's four output rows of each fragment
   int tok;          // token of the lane's row
   float wt;         // routing weight of the lane's row
 };
@@ -501,7 +510,7 @@ __global__ __launch_bounds__(kSliceQuarters * 64) void gemm2_slice_kernel(GemmPa
   const int nsteps = n_items * kSliceSteps;
   const v4f zero = {0.f, 0.f, 0.f, 0.f};
   for (int slice = blockIdx.x; slice < kHiddenSlices; slice += gridDim.x) {
-    const int h0 = slice * 16 * kSliceF;
+    const int h0 = slice * kSliceRows;
     float* my_acc = &acc_lds[q][0][0];
     for (int i = lane; i < T * 16 * kSliceF; i += 64) my_acc[i] = 0.f;
     if (nsteps > 0) {
@@ -517,15 +526,18 @@ __global__ __launch_bounds__(kSliceQuarters * 64) void gemm2_slice_kernel(GemmPa
         const int r = r0 + (m < rows ? m : 0);
 #pragma unroll
         for (int f = 0; f < kSliceF; ++f) {
+          // the lane's hidden row in fragment f (rows past the slice repeat its last row)
+          const int hr = h0 + 16 * f + min(m, kSliceRows - 16 * f - 1);
           if constexpr (PACKED)
-            g.w[f] = load_frag_packed(p.w2 + (((size_t)e * (kHidden / 16) + (h0 >> 4) + f) * kIBlocks + ks) * kPackedFrag +
-                                      lane * 32);
+            g.w[f] = load_frag_packed(p.w2 + (((size_t)e * (kHidden / 16) + (hr >> 4)) * kIBlocks + ks) * kPackedFrag +
+                                      ((hr & 15) + 16 * (lane >> 4)) * 32);
           else
-            g.w[f] = load_frag(p.w2 + ((size_t)e * kHidden + h0 + 16 * f + m) * kInter + ks * 128 + (lane >> 4) * 16);
+            g.w[f] = load_frag(p.w2 + ((size_t)e * kHidden + hr) * kInter + ks * 128 + (lane >> 4) * 16);
+          const int orow = h0 + min(16 * f + 4 * (lane >> 4), kSliceRows - 1);   // first output row
+          g.sw[f] = p.w2_scale[((size_t)e * kHBlocks + orow / kBlock) * kIBlocks + ks];
         }
         g.a = load_frag(p.act + (size_t)r * kInter + ks * 128 + (lane >> 4) * 16);
         g.sa = *reinterpret_cast<const float2*>(p.act_scale + (size_t)r * kQuantBlocks + 2 * ks);
-        g.sw = p.w2_scale[((size_t)e * kHBlocks + h0 / 128) * kIBlocks + ks];
         g.tok = p.sorted_token[r];
         g.wt = p.sorted_weight[r];
       };
@@ -548,9 +560,9 @@ __global__ __launch_bounds__(kSliceQuarters * 64) void gemm2_slice_kernel(GemmPa
           const v4i kZero4 = {0, 0, 0, 0};
           const v8i a_lo = join(lo_half(g.a), kZero4);
           const v8i a_hi = join(kZero4, hi_half(g.a));
-          const float sc_lo = g.sa.x * g.sw, sc_hi = g.sa.y * g.sw;
 #pragma unroll
           for (int f = 0; f < kSliceF; ++f) {
+            const float sc_lo = g.sa.x * g.sw[f], sc_hi = g.sa.y * g.sw[f];
             const v4f d_lo = mfma16x16x128_fp8(g.w[f], a_lo, zero);
             const v4f d_hi = mfma16x16x128_fp8(g.w[f], a_hi, zero);
             acc[f] += d_lo * sc_lo;
@@ -589,9 +601,11 @@ __global__ __launch_bounds__(kSliceQuarters * 64) void gemm2_slice_kernel(GemmPa
       }
     }
     __syncthreads();
-    // the four K quarters, summed in fixed order: 4 columns of one token per thread
-    for (int i = threadIdx.x; i < T * 4 * kSliceF; i += kSliceQuarters * 64) {
-      const int t = i / (4 * kSliceF), c = 4 * (i % (4 * kSliceF));
+    // the four K quarters, summed in fixed order: 4 columns of one token per thread (the slice's
+    // 28 columns; the accumulators' last 4 hold the repeated rows)
+    constexpr int kChunks = kSliceRows / 4;
+    for (int i = threadIdx.x; i < T * kChunks; i += kSliceQuarters * 64) {
+      const int t = i / kChunks, c = 4 * (i % kChunks);
       const v4f s = ((*reinterpret_cast<const v4f*>(&acc_lds[0][t][c]) + *reinterpret_cast<const v4f*>(&acc_lds[1][t][c])) +
                      *reinterpret_cast<const v4f*>(&acc_lds[2][t][c])) +
                     *reinterpret_cast<const v4f*>(&acc_lds[3][t][c]);
