@@ -161,16 +161,22 @@ class PackedWeightCache:
     eviction, so that a model with more layers than copies never repacks in a loop). No copy is
     built while the current stream is being captured into a HIP graph; a copy that a capture has
     used is never freed (a stale one moves to a retired list), because the graph holds its
-    address. `make(w13, w2)` and `capturing()` are injectable so that the policy is testable
-    without a GPU.
+    address. A copy handed to a stream other than the one that built it is recorded on that
+    stream (Tensor.record_stream), so that dropping a stale copy never lets the allocator reuse
+    its memory while work queued on that stream may still read it. `make(w13, w2)`,
+    `capturing()`, `stream_id()` and `record(packed)` are injectable so that the policy is
+    testable without a GPU.
     """
 
-    def __init__(self, max_sets: int = 4, make=None, capturing=None, storage_ref=None):
+    def __init__(self, max_sets: int = 4, make=None, capturing=None, storage_ref=None, stream_id=None,
+                 record=None):
         from torch.multiprocessing.reductions import StorageWeakRef
         self.max_sets = max_sets
         self._make = make or (lambda w13, w2: pack_weights(w13, w2))
         self._capturing = capturing or torch.cuda.is_current_stream_capturing
         self._ref = storage_ref or (lambda t: StorageWeakRef(t.untyped_storage()))
+        self._stream_id = stream_id or (lambda: torch.cuda.current_stream().cuda_stream)
+        self._record = record or (lambda packed: packed.record_stream(torch.cuda.current_stream(packed.device)))
         self._lock = threading.Lock()
         self._entries = {}
         self._retired = []
@@ -184,10 +190,14 @@ class PackedWeightCache:
         version = (w13._version, w2._version)
         with self._lock:
             capturing = self._capturing()
+            stream = self._stream_id()
             ent = self._entries.get(key)
             if ent is not None and not ent["ref13"].expired() and not ent["ref2"].expired() \
                     and ent["version"] == version:
                 ent["captured"] = ent["captured"] or capturing
+                if stream not in ent["streams"]:
+                    self._record(ent["packed"])
+                    ent["streams"].add(stream)
                 return ent["packed"]
             if capturing:
                 return None
@@ -199,7 +209,7 @@ class PackedWeightCache:
                 return None
             packed = self._make(w13, w2)
             self._entries[key] = dict(ref13=self._ref(w13), ref2=self._ref(w2), version=version, packed=packed,
-                                      captured=False)
+                                      captured=False, streams={stream})
             return packed
 
     def _drop(self, key):

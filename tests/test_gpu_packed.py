@@ -144,3 +144,38 @@ def test_run_keeps_a_packed_copy_per_weight_set():
         assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
     finally:
         moe._packed_weights = saved
+
+
+def test_run_on_a_second_stream_uses_the_copy():
+    """run() on a side stream with a copy built on another: the copy is recorded on the side stream
+    (Tensor.record_stream) and the result is the row-major one, bit for bit."""
+    gh = _gh()
+    moe = gh.pkg.moe
+    dev = torch.device("cuda:0")
+    w = gh.inputs.make_weights(517, dev, experts=32)
+    T = 20
+    logits, bias, hq, hs = gh.inputs.make_activations(T, 6300, dev)
+    kw = dict(routing_logits=logits, routing_bias=bias, hidden_states=hq, hidden_states_scale=hs,
+              gemm1_weights=w[0], gemm1_weights_scale=w[1], gemm2_weights=w[2], gemm2_weights_scale=w[3],
+              local_expert_offset=0, routed_scaling_factor=2.5)
+    ref = torch.empty((T, 7168), dtype=torch.bfloat16, device=dev)
+    gh.run_layer(gh.make_args(**kw, output=ref), gh.new_workspace(T, dev))
+    cache = moe.PackedWeightCache()
+    saved = moe._packed_weights
+    moe._packed_weights = cache
+    try:
+        out = torch.empty_like(ref)
+        gh.pkg.run(**kw, output=out)                      # builds the copy on the current stream
+        side = torch.cuda.Stream(device=dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        out2 = torch.empty_like(ref)
+        with torch.cuda.stream(side):
+            gh.pkg.run(**kw, output=out2)
+        torch.cuda.current_stream(dev).wait_stream(side)
+        torch.cuda.synchronize()
+        ent = next(iter(cache._entries.values()))
+        assert len(ent["streams"]) == 2
+        assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+        assert torch.equal(out2.view(torch.int16), ref.view(torch.int16))
+    finally:
+        moe._packed_weights = saved

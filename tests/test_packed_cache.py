@@ -27,7 +27,10 @@ class Recorder:
 
 
 def _cache(moe, rec, max_sets=2):
-    return moe.PackedWeightCache(max_sets=max_sets, make=rec.make, capturing=lambda: rec.capturing)
+    rec.stream = 1
+    rec.recorded = []
+    return moe.PackedWeightCache(max_sets=max_sets, make=rec.make, capturing=lambda: rec.capturing,
+                                 stream_id=lambda: rec.stream, record=lambda p: rec.recorded.append((p, rec.stream)))
 
 
 def _set():
@@ -100,3 +103,26 @@ def test_off_and_clear(moe):
     c.get(w13, w2)
     c.clear()
     assert len(c) == 0 and c.get(w13, w2) is rec.built[1]
+
+
+def test_other_streams_are_recorded_once(moe):
+    """A copy used on a stream other than its builder's is recorded there (record_stream) once, so
+    that dropping it never frees memory that work queued on that stream may still read."""
+    rec = Recorder()
+    c = _cache(moe, rec)
+    w13, w2 = _set()
+    p = c.get(w13, w2)             # built on stream 1: nothing to record
+    assert c.get(w13, w2) is p and rec.recorded == []
+    rec.stream = 2
+    assert c.get(w13, w2) is p and rec.recorded == [(p, 2)]
+    c.get(w13, w2)
+    rec.stream = 1
+    c.get(w13, w2)
+    assert rec.recorded == [(p, 2)]
+    # a rebuilt copy starts over on the stream that builds it
+    w13.add_(1)
+    rec.stream = 3
+    q = c.get(w13, w2)
+    assert q is not p and rec.recorded == [(p, 2)]
+    rec.stream = 1
+    assert c.get(w13, w2) is q and rec.recorded == [(p, 2), (q, 1)]
