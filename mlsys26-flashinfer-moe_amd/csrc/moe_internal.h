@@ -7,8 +7,7 @@
 //   T <= 64 (moe_fp8_run): route_wide_kernel -> gemm1_stream_dispatch_kernel (GEMM1 that
 //   rebuilds the dispatch itself) -> requant_kernel -> gemm2_slice_kernel (GEMM2 and the
 //   combine); otherwise
-//   (route_wide_kernel (T <= 64) | route_kernel<false>) -> dispatch_small_kernel
-//   | (route_kernel<true> -> place_kernel)
+//   route_wide_kernel -> dispatch_small_kernel (T <= 256) | route_kernel -> place_kernel
 //   -> GEMM1 -> [requant_kernel] -> GEMM2 -> [combine_kernel]
 // where, with <= 32 rows per work item, GEMM1 is gemm_stream_kernel<1> and leaves fp32 SwiGLU
 // rows for requant_kernel, and GEMM2 is gemm2_slice_kernel (16-row items, up to 64 tokens)
@@ -38,7 +37,7 @@ constexpr int kIBlocks = MOE_FP8_I_BLOCKS;     // 16
 // Routing: up to kWideRouteTokens tokens one token per wavefront (4 per work-group), above
 // that 16 lanes per token and 16 tokens per work-group of 4 wavefronts; the one-work-group
 // dispatch of small batches uses 1024 threads.
-constexpr int kWideRouteTokens = 64;
+constexpr int kWideRouteTokens = 256;
 constexpr int kRouteTokensPerBlock = 16;
 constexpr int kRouteThreads = 1024;
 // Up to this many tokens routing and dispatch run in a single work-group (one launch).

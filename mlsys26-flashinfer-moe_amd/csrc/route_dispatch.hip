@@ -1,15 +1,15 @@
 // Routing and dispatch for the fused MoE layer (gfx950).
 //
 // The DeepSeek-V3 no-aux grouped routing (kernel.py:428-542) runs with branch-free DPP
-// reductions: up to 64 tokens one token per wavefront (route_wide_kernel: 4 experts per lane,
+// reductions: up to 256 tokens one token per wavefront (route_wide_kernel: 4 experts per lane,
 // the shortest dependent chain per token), above that sixteen lanes per token and four
-// tokens per wavefront (route_kernel). Dispatch then histograms the local assignments, scans
+// tokens per wavefront (route_kernel, which also records per-work-group histograms and ranks
+// for the multi-work-group dispatch). Dispatch then histograms the local assignments, scans
 // them into CSR offsets, builds the GEMM work list and places every assignment in its bucket:
-//   T <= 64:  route_wide_kernel -> dispatch_small_kernel, which does the whole dispatch in one
-//             work-group, in LDS (moe_fp8_run rebuilds the dispatch inside GEMM1 instead);
-//   T <= 256 (or given top-k lists): route_kernel<false> (16 tokens per work-group) ->
-//             dispatch_small_kernel;
-//   larger T: route_kernel<true> (also per work-group histograms and ranks) -> place_kernel
+//   T <= 256 (or given top-k lists): route_wide_kernel -> dispatch_small_kernel, which does the
+//             whole dispatch in one work-group, in LDS (up to 64 tokens moe_fp8_run rebuilds the
+//             dispatch inside GEMM1 instead);
+//   larger T: route_kernel (also per work-group histograms and ranks) -> place_kernel
 //             (each work-group reduces the histograms it needs). No kernel synchronises
 //             across work-groups.
 //
@@ -378,12 +378,11 @@ __device__ __forceinline__ void finish_counts(const RouteParams& p, int e, int r
 
 }  // namespace
 
-// Routing (or, on given top-k lists, loading) of 16 tokens per work-group of 4 wavefronts.
-// With RANKS the work-group also records every token's local count, the stable rank of
-// each local slot among its 128 slots and its expert histogram (dispatch of large batches).
+// Routing (or, on given top-k lists, loading) of 16 tokens per work-group of 4 wavefronts for
+// the dispatch of large batches: the work-group also records every token's local count, the
+// stable rank of each local slot among its 128 slots and its expert histogram.
 constexpr int kRouteWaves = kRouteTokensPerBlock / 4;
 
-template <bool RANKS>
 __global__ __launch_bounds__(kRouteWaves * 64) void route_kernel(RouteParams p) {
   __shared__ __attribute__((aligned(16))) float s_bias[kExpertsGlobal];
   __shared__ int s_le[kRouteTokensPerBlock * kTopK];
@@ -410,7 +409,7 @@ __global__ __launch_bounds__(kRouteWaves * 64) void route_kernel(RouteParams p) 
   } else if (slot_lane) {
     id = p.topk_ids[t * kTopK + r];
   }
-  if constexpr (RANKS) {
+  {
     const int le = slot_lane ? local_of(id, p.offset) : -1;
     const uint64_t m = __ballot(le >= 0);
     if (r == 0 && t < p.T) p.token_nlocal[t] = __popcll((m >> (lane & 48)) & 0xFFull);
@@ -590,12 +589,12 @@ __global__ __launch_bounds__(kPlaceThreads) void place_kernel(RouteParams p) {
   p.sorted_slot[pos] = s;
 }
 
-// top-k lists only (no dispatch)
+// top-k lists only (no dispatch), for batches of up to kWideRouteTokens tokens
+static_assert(kWideRouteTokens >= kSinglePassTokens && kWideRouteTokens >= kFusedDispatchTokens,
+              "every batch routed without ranks fits route_wide_kernel");
 static hipError_t launch_route_lists(const RouteParams& p, hipStream_t s) {
-  if (p.T <= kWideRouteTokens)
-    hipLaunchKernelGGL(route_wide_kernel, dim3((p.T + 3) / 4), dim3(256), 0, s, p);
-  else
-    hipLaunchKernelGGL(route_kernel<false>, dim3(p.nblocks), dim3(kRouteWaves * 64), 0, s, p);
+  if (p.T > kWideRouteTokens) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(route_wide_kernel, dim3((p.T + 3) / 4), dim3(256), 0, s, p);
   return hipGetLastError();
 }
 
@@ -606,7 +605,7 @@ hipError_t launch_route_dispatch(const RouteParams& p, hipStream_t s) {
     if (!p.skip_routing && launch_route_lists(p, s) != hipSuccess) return hipGetLastError();
     hipLaunchKernelGGL(dispatch_small_kernel, dim3(1), dim3(kRouteThreads), 0, s, p);
   } else {
-    hipLaunchKernelGGL(route_kernel<true>, dim3(p.nblocks), dim3(kRouteWaves * 64), 0, s, p);
+    hipLaunchKernelGGL(route_kernel, dim3(p.nblocks), dim3(kRouteWaves * 64), 0, s, p);
     hipLaunchKernelGGL(place_kernel, dim3(p.nblocks), dim3(kPlaceThreads), 0, s, p);
   }
   return hipGetLastError();

@@ -1,8 +1,8 @@
 """GPU parity of routing + dispatch (moe_fp8_route_dispatch) against the oracle.
 
-Up to 64 tokens a wavefront routes one token (route_wide_kernel, the routing moe_fp8_run uses
-at those sizes); above, sixteen lanes route one token (route_kernel). Both are checked on the
-golden router logits, every bias dtype, ties and extreme values.
+Up to 256 tokens a wavefront routes one token (route_wide_kernel); above, sixteen lanes route one
+token (route_kernel, which also ranks the slots for the multi-work-group dispatch). Both are
+checked on the golden router logits, every bias dtype, ties and extreme values.
 
 Bar: bit-exact. Expert ids, routing weights (as fp32 bit patterns), histogram, CSR
 offsets, the stable bucket permutation, per-token local counts and the GEMM work list
@@ -56,8 +56,24 @@ def test_routing_bit_exact_on_golden_logits(part):
 
 
 @pytest.mark.parametrize("part", [0, 1, 2])
+def test_routing_bit_exact_on_golden_logits_large_batches(part):
+    """Above 256 tokens sixteen lanes route a token (route_kernel): the golden rows of each bias
+    set repeated to 3x their count."""
+    m = GOLD["bias_index"] == part
+    logits, bias = np.concatenate([GOLD["logits"][m]] * 3), GOLD["bias_sets"][part]
+    T = logits.shape[0]
+    assert T > 256
+    ws, gh = _route_gpu(logits, bias)
+    rid, rw = orouting.route(logits, bias, 2.5)
+    assert np.array_equal(gh.read(ws, "topk_ids", torch.int32, T * 8).reshape(T, 8), rid)
+    assert np.array_equal(gh.read(ws, "topk_weights", torch.float32, T * 8).reshape(T, 8).view(np.uint32),
+                          rw.view(np.uint32))
+    gh.check_dispatch(ws, rid, rw, 0, T)
+
+
+@pytest.mark.parametrize("part", [0, 1, 2])
 def test_routing_bit_exact_on_golden_logits_small_batches(part):
-    """Up to 64 tokens a wavefront routes one token (route_wide_kernel): the golden rows of each
+    """Up to 256 tokens a wavefront routes one token (route_wide_kernel): the golden rows of each
     bias set in batches of 64 and of 1."""
     m = GOLD["bias_index"] == part
     logits_all, bias = GOLD["logits"][m], GOLD["bias_sets"][part]
@@ -72,7 +88,7 @@ def test_routing_bit_exact_on_golden_logits_small_batches(part):
                                   rw.view(np.uint32))
 
 
-@pytest.mark.parametrize("T", [40, 77])
+@pytest.mark.parametrize("T", [40, 77, 300])
 @pytest.mark.parametrize("bias_dtype", [torch.float32, torch.bfloat16, torch.float16])
 def test_routing_bias_dtypes(bias_dtype, T):
     rng = np.random.default_rng(21)
@@ -86,7 +102,9 @@ def test_routing_bias_dtypes(bias_dtype, T):
                           rw.view(np.uint32))
 
 
-def test_routing_ties_and_extremes():
+@pytest.mark.parametrize("repeat", [1, 50])
+def test_routing_ties_and_extremes(repeat):
+    """Six special rows (T = 6: route_wide_kernel), and the same rows 50 times (T = 300: route_kernel)."""
     T = 6
     logits = np.zeros((T, 256), np.float32)
     logits[1] = 100.0                       # saturated sigmoid: all ties at 1.0
@@ -96,6 +114,8 @@ def test_routing_ties_and_extremes():
     logits[5] = np.linspace(-50, 50, 256, dtype=np.float32)
     bias = np.zeros(256, np.float32)
     bias[200] = -np.inf                     # an expert that can never win unless forced
+    logits = np.concatenate([logits] * repeat)
+    T = logits.shape[0]
     ws, gh = _route_gpu(logits, bias, rsf=1.0)
     rid, rw = orouting.route(logits, bias, 1.0)
     assert np.array_equal(gh.read(ws, "topk_ids", torch.int32, T * 8).reshape(T, 8), rid)
