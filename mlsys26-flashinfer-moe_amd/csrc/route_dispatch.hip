@@ -9,7 +9,8 @@
 //   T <= 256 (or given top-k lists): route_wide_kernel -> dispatch_small_kernel, which does the
 //             whole dispatch in one work-group, in LDS (up to 64 tokens moe_fp8_run rebuilds the
 //             dispatch inside GEMM1 instead);
-//   larger T: route_kernel (also per work-group histograms and ranks) -> place_kernel
+//   larger T: route_kernel (also per work-group histograms and ranks) -> place_kernel (above
+//             16384 tokens with block_scan_kernel between them, which keeps the cost linear in T)
 //             (each work-group reduces the histograms it needs). No kernel synchronises
 //             across work-groups.
 //
@@ -527,6 +528,11 @@ constexpr int kPlaceThreads = 512;
 constexpr int kPlaceGroups = kPlaceThreads / kExpertsLocal;   // 16
 static_assert(kRouteTokensPerBlock * kTopK <= kPlaceThreads, "one slot per thread");
 
+// SCANNED (batches of more than kPlaceDirectBlocks routing work-groups): block_scan_kernel has
+// already turned block_count into per-work-group exclusive prefixes and written the CSR
+// offsets, so that each work-group reads its 32 prefixes instead of reducing every
+// histogram (which costs O(work-groups^2) in all).
+template <bool SCANNED>
 __global__ __launch_bounds__(kPlaceThreads) void place_kernel(RouteParams p) {
   __shared__ int s_pre[kPlaceGroups][kExpertsLocal];
   __shared__ int s_tot[kPlaceGroups][kExpertsLocal];
@@ -542,6 +548,17 @@ __global__ __launch_bounds__(kPlaceThreads) void place_kernel(RouteParams p) {
   const int rank = le >= 0 ? p.slot_rank[s] : 0;
   const float w = le >= 0 ? p.topk_w[s] : 0.f;
 
+  if constexpr (SCANNED) {
+    if (tid < kExpertsLocal) s_prefix[tid] = p.block_count[b * kExpertsLocal + tid];
+    if (tid <= kExpertsLocal) s_start[tid] = p.expert_start[tid];
+    __syncthreads();
+    if (le < 0) return;
+    const int pos = s_start[le] + s_prefix[le] + rank;
+    p.sorted_token[pos] = s / kTopK;
+    p.sorted_weight[pos] = w;
+    p.sorted_slot[pos] = s;
+    return;
+  }
   const int e = tid % kExpertsLocal, j = tid / kExpertsLocal;
   int pre = 0, tot = 0;
   for (int b0 = j; b0 < nb; b0 += kPlaceGroups * kScanBatch) {
@@ -589,6 +606,55 @@ __global__ __launch_bounds__(kPlaceThreads) void place_kernel(RouteParams p) {
   p.sorted_slot[pos] = s;
 }
 
+// Per-expert exclusive prefix of the routing work-groups' histograms, for batches of more than
+// kPlaceDirectBlocks routing work-groups: one work-group of 1024 threads, thread (j, e) owning
+// expert e's counts in the j-th of 32 contiguous ranges of work-groups. block_count is
+// rewritten in place with the prefixes, and lanes 0..31 then write the CSR offsets, counters
+// and work list (finish_counts) from the totals. O(work-groups) loads in all.
+constexpr int kPlaceDirectBlocks = 1024;
+constexpr int kBlockScanThreads = 1024;
+constexpr int kBlockScanRanges = kBlockScanThreads / kExpertsLocal;   // 32
+
+__global__ __launch_bounds__(kBlockScanThreads) void block_scan_kernel(RouteParams p) {
+  __shared__ int s_sum[kBlockScanRanges][kExpertsLocal];
+  __shared__ int s_start[kExpertsLocal + 1];
+  const int tid = threadIdx.x;
+  const int e = tid % kExpertsLocal, j = tid / kExpertsLocal;
+  const int nb = p.nblocks;
+  const int per = (nb + kBlockScanRanges - 1) / kBlockScanRanges;
+  const int b0 = min(j * per, nb), b1 = min(b0 + per, nb);
+  int sum = 0;
+  for (int b = b0; b < b1; b += kScanBatch) {
+    int v[kScanBatch];
+#pragma unroll
+    for (int i = 0; i < kScanBatch; ++i) v[i] = b + i < b1 ? p.block_count[(b + i) * kExpertsLocal + e] : 0;
+#pragma unroll
+    for (int i = 0; i < kScanBatch; ++i) sum += v[i];
+  }
+  s_sum[j][e] = sum;
+  __syncthreads();
+  int pre = 0, tot = 0;
+#pragma unroll
+  for (int jj = 0; jj < kBlockScanRanges; ++jj) {
+    const int v = s_sum[jj][e];
+    tot += v;
+    pre += jj < j ? v : 0;
+  }
+  int run = pre;
+  for (int b = b0; b < b1; b += kScanBatch) {
+    int v[kScanBatch];
+#pragma unroll
+    for (int i = 0; i < kScanBatch; ++i) v[i] = b + i < b1 ? p.block_count[(b + i) * kExpertsLocal + e] : 0;
+#pragma unroll
+    for (int i = 0; i < kScanBatch; ++i)
+      if (b + i < b1) {
+        p.block_count[(b + i) * kExpertsLocal + e] = run;
+        run += v[i];
+      }
+  }
+  if (tid < kExpertsLocal) finish_counts(p, tid, tot, s_start);
+}
+
 // top-k lists only (no dispatch), for batches of up to kWideRouteTokens tokens
 static_assert(kWideRouteTokens >= kSinglePassTokens && kWideRouteTokens >= kFusedDispatchTokens,
               "every batch routed without ranks fits route_wide_kernel");
@@ -606,7 +672,12 @@ hipError_t launch_route_dispatch(const RouteParams& p, hipStream_t s) {
     hipLaunchKernelGGL(dispatch_small_kernel, dim3(1), dim3(kRouteThreads), 0, s, p);
   } else {
     hipLaunchKernelGGL(route_kernel, dim3(p.nblocks), dim3(kRouteWaves * 64), 0, s, p);
-    hipLaunchKernelGGL(place_kernel, dim3(p.nblocks), dim3(kPlaceThreads), 0, s, p);
+    if (p.nblocks > kPlaceDirectBlocks) {
+      hipLaunchKernelGGL(block_scan_kernel, dim3(1), dim3(kBlockScanThreads), 0, s, p);
+      hipLaunchKernelGGL(place_kernel<true>, dim3(p.nblocks), dim3(kPlaceThreads), 0, s, p);
+    } else {
+      hipLaunchKernelGGL(place_kernel<false>, dim3(p.nblocks), dim3(kPlaceThreads), 0, s, p);
+    }
   }
   return hipGetLastError();
 }

@@ -124,8 +124,11 @@ def test_routing_ties_and_extremes(repeat):
 
 
 @pytest.mark.parametrize("T,offset", [(1, 0), (5, 224), (16, 0), (17, 64), (64, 0), (255, 32),
-                                      (256, 0), (257, 0), (1000, 250), (4096, 0), (8192, 96), (3, -3)])
+                                      (256, 0), (257, 0), (1000, 250), (4096, 0), (8192, 96), (3, -3),
+                                      (16384, 0), (16385, 32), (65536, 96)])
 def test_dispatch_matches_oracle(T, offset):
+    """Above 16384 tokens (1024 routing work-groups) the per-work-group prefixes come from
+    block_scan_kernel instead of every placing work-group's own reduction."""
     rng = np.random.default_rng(T * 7 + offset + 1000)
     logits = rng.standard_normal((T, 256)).astype(np.float32)
     bias = (rng.standard_normal(256) * 0.1).astype(np.float32)
