@@ -9,7 +9,8 @@
 // 16 lanes per token row, 8 elements per lane (one 16- or 32-byte load, one 8-byte store),
 // the block's amax reduced over its 16 lanes, and the 16 scales written as one 64-byte
 // segment of the token-minor scale array. Consecutive work-groups take neighbouring blocks
-// of the same rows.
+// of the same rows. Four blocks per work-group (their loads in flight together, a quarter of
+// the work-groups) measured slower: T=8192 35.8 against 33.1 us, T=1024 8.1 against 6.2.
 #include <hip/hip_fp16.h>
 
 #include "moe_internal.h"
