@@ -313,6 +313,30 @@ def test_cpu_output_and_inputs_are_moved():
     assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
 
 
+@pytest.mark.parametrize("name", ["t16", "t1024_off64"])
+def test_strided_inputs_give_the_same_output(name):
+    """run() takes the reference's contract with any strides (it makes its inputs contiguous, as
+    kernel.py's .contiguous() calls do): logits, hidden states and their scales passed as strided
+    views give the contiguous call's output bit for bit."""
+    gh = _gh()
+    kw, _ = _workload(name)
+    T = kw["hidden_states"].shape[0]
+    ref = _run_full(kw)
+    wide = torch.zeros((T, 512), dtype=kw["routing_logits"].dtype, device=ref.device)
+    wide[:, 128:384] = kw["routing_logits"]
+    hid = torch.zeros((T, 2 * 7168), dtype=torch.uint8, device=ref.device)
+    hid[:, 7168:] = kw["hidden_states"].view(torch.uint8)
+    sc_t = kw["hidden_states_scale"].t().contiguous()          # [T, 56]: its transpose is a strided [56, T]
+    kw2 = dict(kw, routing_logits=wide[:, 128:384], hidden_states=hid[:, 7168:].view(torch.float8_e4m3fn),
+               hidden_states_scale=sc_t.t())
+    assert not kw2["routing_logits"].is_contiguous() and not kw2["hidden_states"].is_contiguous()
+    assert not kw2["hidden_states_scale"].is_contiguous()
+    out = torch.full_like(ref, float("nan"))
+    gh.pkg.run(**kw2, output=out)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+
+
 def _given_topk(case, T, rng):
     ids = np.stack([rng.permutation(256)[:8] for _ in range(T)]).astype(np.int32)
     if case == "one_expert":                     # every token on local expert 5, nothing else local
