@@ -42,10 +42,14 @@ constexpr int kStreamWaves = 4;                      // wavefronts per work-grou
 // and depth of the register ring.
 //   GEMM1: a unit is 16 SwiGLU columns = their 16 gate rows + 16 up rows (2 fragments).
 //   GEMM2: a unit is 64 hidden rows (4 fragments).
-// GEMM1 uses a 3-slot ring (two K-steps in flight per wavefront, 130 registers with the
-// accumulators), GEMM2 a 2-slot ring (136 registers): three wavefronts per SIMD, so that at decode sizes every unit
-// has its own wavefront and the grid drains in one round (measured at T=64: GEMM1
-// 117 -> 109 us, GEMM2 64 -> 57 us against 4-slot rings and 32-row GEMM2 units).
+// Both use a 2-slot ring (one K-step in flight per wavefront besides the one consumed; GEMM1
+// 96 registers with the accumulators, GEMM2 136), so that at decode sizes every unit has its own
+// wavefront and the grid drains in one round. The whole chip then keeps ~15 MB of weight loads
+// in flight; a plain HBM read peaks at 6-8 MB in flight and slows beyond. Measured at T=64:
+// GEMM1 117 -> 109 us and GEMM2 64 -> 57 us against 4-slot rings and 32-row GEMM2 units; GEMM1
+// with 2 slots against 3: bit-identical, 1 us faster at T=16 and T=64, 1.5-3.6 us at T=96-256;
+// capping the resident work-groups to cut the loads in flight further (2 or 3 per CU) was
+// slower (T=64 GEMM1 110.8 / 108.6 against 105.8 us).
 // Requantising GEMM1's fp32 rows inside GEMM2 instead of in requant_kernel was measured
 // and is slower (T=64: GEMM2 + combine 68 -> 80 us): the per-element IEEE divisions, four
 // times the activation bytes and fewer resident wavefronts cost more than the launch.
@@ -56,7 +60,7 @@ struct StreamShape<kG1> {
   static constexpr int kSteps = kHBlocks;   // K = 7168
   static constexpr int kFrags = 2;
   static constexpr int kSlices = kInter / 16;
-  static constexpr int kRing = 3;
+  static constexpr int kRing = 2;
 };
 template <>
 struct StreamShape<kG2> {
