@@ -473,7 +473,8 @@ __global__ __launch_bounds__(256) void requant_kernel(GemmParams p) {
 // expert (the zero-fill and finalize of kernel.py:704, 729). Deterministic, no atomics.
 // 28-row slices against 32-row ones (224 work-groups, 32 CUs idle): every output element is
 // computed by the same operations in the same order, and the weight stream spreads over all
-// 256 CUs.
+// 256 CUs. A 2-slot ring against 4 (3 steps in flight): bit-identical, 240 registers instead of
+// 312, T=16 GEMM2 34.0 -> 33.4 us, T=64 unchanged.
 // Slice width, measured at T=64 / T=16 (GEMM2 with the requantisation before it, us): one
 // fragment 78.0 / 39.8, two 63.9 / 33.7, four 101.6 / 52.6, against 68.0 / 40.0 for the
 // wavefront-per-unit GEMM2 plus combine_kernel. One fragment spends a 2 KB activation
@@ -483,13 +484,13 @@ constexpr int kSliceF = 2;                               // weight fragments per
 constexpr int kSliceRows = 28;                           // hidden rows per work-group
 constexpr int kSliceQuarters = 4;                        // wavefronts per work-group = K quarters
 constexpr int kSliceSteps = kIBlocks / kSliceQuarters;   // 4 K-steps per quarter and item
-constexpr int kSliceRing = kSliceSteps;                  // ring slots: 3 steps in flight
+constexpr int kSliceRing = 2;                            // ring slots: 1 step in flight besides the one consumed
 constexpr int kHiddenSlices = kHidden / kSliceRows;      // 256
 static_assert(kHidden % kSliceRows == 0 && kSliceRows > 16 * (kSliceF - 1) && kSliceRows <= 16 * kSliceF,
               "slice rows");
 // a lane's four output rows of a fragment are 4-aligned, so they share one 128-row W2 scale block
 static_assert(kSliceRows % 4 == 0 && kBlock % 4 == 0, "scale blocks");
-static_assert(kSliceRing == kSliceSteps, "one ring turn per item: slot u is K-step u of the item");
+static_assert(kSliceSteps % kSliceRing == 0, "slot u % ring is K-step u of the item");
 static_assert(kFusedItems <= 64, "one work item per lane");
 
 struct SliceStage {
@@ -557,7 +558,7 @@ __global__ __launch_bounds__(kSliceQuarters * 64) void gemm2_slice_kernel(GemmPa
         for (int u = 0; u < kSliceSteps; ++u) {
           issue(st0 + u + kSliceRing - 1, ring[(u + kSliceRing - 1) % kSliceRing]);
           __builtin_amdgcn_sched_barrier(0);
-          const SliceStage& g = ring[u];
+          const SliceStage& g = ring[u % kSliceRing];
           // the act fragment's two 64-column halves carry their own scales: one MFMA per
           // half, the other half's bytes zeroed (lanes hold bytes [16j, 16j+16) of the first
           // half in a[0..3] and of the second in a[4..7])
@@ -577,7 +578,7 @@ __global__ __launch_bounds__(kSliceQuarters * 64) void gemm2_slice_kernel(GemmPa
         // end of the item: its weighted rows into this wavefront's token accumulators; when a
         // token names a local expert more than once its rows are adjacent (slot order), and
         // the first one adds the others in order, so that each accumulator has one writer
-        const SliceStage& g = ring[kSliceSteps - 1];
+        const SliceStage& g = ring[(kSliceSteps - 1) % kSliceRing];
         const int rows = __builtin_amdgcn_readlane(my_item.z, st0 / kSliceSteps);
         const bool live = m < rows;
         const int prev = __shfl(g.tok, lane - 1);
