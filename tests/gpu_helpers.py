@@ -1,8 +1,6 @@
 """Helpers for the GPU parity tests: run the C-ABI stages and read the workspace."""
 from __future__ import annotations
 
-import ctypes
-
 import numpy as np
 import torch
 
