@@ -49,7 +49,9 @@ constexpr int kStreamWaves = 4;                      // wavefronts per work-grou
 // GEMM1 117 -> 109 us and GEMM2 64 -> 57 us against 4-slot rings and 32-row GEMM2 units; GEMM1
 // with 2 slots against 3: bit-identical, 1 us faster at T=16 and T=64, 1.5-3.6 us at T=96-256;
 // capping the resident work-groups to cut the loads in flight further (2 or 3 per CU) was
-// slower (T=64 GEMM1 110.8 / 108.6 against 105.8 us).
+// slower (T=64 GEMM1 110.8 / 108.6 against 105.8 us). GEMM1 units of 32 columns (4
+// fragments sharing one activation fragment per K-step, half as many units) were bit-identical
+// and slower: T=64 110.3 against 105.5 us, T=16 55.6 against 54.3.
 // Requantising GEMM1's fp32 rows inside GEMM2 instead of in requant_kernel was measured
 // and is slower (T=64: GEMM2 + combine 68 -> 80 us): the per-element IEEE divisions, four
 // times the activation bytes and fewer resident wavefronts cost more than the launch.
