@@ -293,8 +293,11 @@ def test_tile_stage_repeated(name):
     assert torch.equal(whole.view(torch.int16), out.view(torch.int16)), "staged and whole-layer runs differ"
 
 
-@pytest.mark.parametrize("name", ["t64", "t1024_off64"])
+@pytest.mark.parametrize("name", ["t64", "t1024_off64", "t8192", "t4096_skew"])
 def test_deterministic_and_fp32_output(name):
+    """Two calls give the same bits, also where the tile kernels' work-groups take their units
+    from per-XCD counters (a different unit-to-CU assignment on every call), and the fp32
+    output rounds to the bf16 one."""
     kw, npkw = _workload(name)
     a = _run_full(kw)
     b = _run_full(kw)
