@@ -27,6 +27,8 @@ The layer is checked in two halves and as a whole, on bf16 output compared as fl
 Sizes: T from 1 to 32768 (the largest puts parked GEMM2 rows beyond 2 GiB of the workspace);
 T=8192 and the skewed T=4096 batch are checked on 256 sampled tokens each.
 """
+import re
+
 import numpy as np
 import pytest
 import torch
@@ -65,15 +67,23 @@ def _workload(name):
     gh = _gh()
     dev = torch.device("cuda:0")
     w, wnp = _weights()
-    if name in ("t256", "t32768"):
+    odd = re.fullmatch(r"t(\d+)_off(m?)(\d+)", name) if name not in gh.inputs.WORKLOADS else None
+    if name in ("t256", "t32768") or odd:
         # t256: a decode batch between the named workloads (32-row items, separate
         # requantisation); t32768: a long prefill whose parked GEMM2 rows lie beyond 2 GiB of
-        # the workspace (64-bit offsets in GEMM2 and the combine)
-        T, seed = (256, 1005) if name == "t256" else (32768, 1006)
+        # the workspace (64-bit offsets in GEMM2 and the combine); t<T>_off<o>: local expert
+        # windows that reach past expert 255 or start below 0 ("m": negative), so that only part
+        # of the 32 local experts exist
+        offset = 0
+        if odd:
+            T, seed = int(odd[1]), 1100 + int(odd[1])
+            offset = -int(odd[3]) if odd[2] else int(odd[3])
+        else:
+            T, seed = (256, 1005) if name == "t256" else (32768, 1006)
         logits, bias, hq, hs = gh.inputs.make_activations(T, seed, dev)
         kw = dict(routing_logits=logits, routing_bias=bias, hidden_states=hq, hidden_states_scale=hs,
                   gemm1_weights=w[0], gemm1_weights_scale=w[1], gemm2_weights=w[2], gemm2_weights_scale=w[3],
-                  local_expert_offset=0, routed_scaling_factor=gh.inputs.ROUTED_SCALING_FACTOR)
+                  local_expert_offset=offset, routed_scaling_factor=gh.inputs.ROUTED_SCALING_FACTOR)
     else:
         kw = gh.inputs.make_workload(name, dev, weights=w)
     npkw = gh.to_numpy_inputs({**kw, "gemm1_weights": w[0][:1], "gemm2_weights": w[2][:1]})
@@ -148,7 +158,8 @@ def _wanted_rows(emu, tokens):
 
 
 @pytest.mark.parametrize("name,sample", [("t16", None), ("t64", None), ("t256", None), ("t1024_off64", None),
-                                         ("t8192", 256), ("t4096_skew", 256), ("t32768", 24)])
+                                         ("t8192", 256), ("t4096_skew", 256), ("t32768", 24),
+                                         ("t40_off240", None), ("t100_off240", None), ("t300_offm16", None)])
 def test_layer_matches_oracle(name, sample):
     gh = _gh()   # registers the package
     from mlsys26_flashinfer_moe_amd import moe
