@@ -11,8 +11,10 @@
  * host<->device synchronisation and allocates no memory: all temporaries live in a
  * caller-owned workspace of moe_fp8_workspace_bytes(T) bytes. Pointers are device
  * pointers to contiguous row-major buffers. Return value: 0 on success, a negative
- * MOE_FP8_E* code otherwise (moe_fp8_strerror() gives the text); on error nothing
- * has been launched.
+ * MOE_FP8_E* code otherwise (moe_fp8_strerror() gives the text). Arguments are checked
+ * before anything is launched, so on every error but MOE_FP8_ELAUNCH nothing has been
+ * launched; MOE_FP8_ELAUNCH reports a launch that HIP rejected, possibly after earlier
+ * kernels of the same call were queued (the output is then undefined).
  *
  * Reference interface replaced: run() in kernel.py:562-729 (nikhilnd/mlsys26-flashinfer-moe),
  * and the stages it calls (kernel.py:624-639 routing, 649-661 dispatch and tile schedule,
