@@ -434,6 +434,58 @@ def test_layer_edge_cases_given_topk(T, case):
         assert np.all(got[640:] == 0)
 
 
+@pytest.mark.parametrize("T,offset", [(3, 0), (33, 160), (65, 32), (129, 224), (257, 96), (511, 0),
+                                      (1000, 64), (2047, 128), (4097, 192), (9001, 0)])
+def test_odd_batches_match_oracle(T, offset):
+    """Batch sizes away from the named workloads and from powers of two, on several local
+    expert windows, through moe_fp8_run on a fresh workspace: top-k lists and the dispatch
+    bit-exact, the intermediate and GEMM2 + combine within the per-element bounds above, the
+    output within the emulated oracle's relative RMS, tokens without a local expert exactly
+    zero, and a second call bit-identical."""
+    gh = _gh()
+    dev = torch.device("cuda:0")
+    w, wnp = _weights()
+    print(f"odd batch T={T} offset={offset}", flush=True)
+    rsf = gh.inputs.ROUTED_SCALING_FACTOR
+    logits, bias, hq, hs = gh.inputs.make_activations(T, 4000 + T + offset, dev)
+    kw = dict(routing_logits=logits, routing_bias=bias, hidden_states=hq, hidden_states_scale=hs,
+              gemm1_weights=w[0], gemm1_weights_scale=w[1], gemm2_weights=w[2], gemm2_weights_scale=w[3],
+              local_expert_offset=offset, routed_scaling_factor=rsf)
+    outs = []
+    for _ in range(2):
+        out = torch.full((T, 7168), float("nan"), dtype=torch.bfloat16, device=dev)
+        ws = gh.new_workspace(T, dev)
+        gh.run_layer(gh.make_args(**kw, output=out), ws)
+        torch.cuda.synchronize()
+        outs.append(out)
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16)), "two calls differ bitwise"
+    got = outs[1].float().cpu().numpy()
+    assert np.isfinite(got).all()
+    ids = gh.read(ws, "topk_ids", torch.int32, T * 8).reshape(T, 8)
+    wts = gh.read(ws, "topk_weights", torch.float32, T * 8).reshape(T, 8)
+    rid, rw = orouting.route(logits.cpu().numpy(), bias.float().cpu().numpy(), rsf)
+    assert np.array_equal(ids, rid)
+    assert np.array_equal(wts.view(np.uint32), rw.view(np.uint32))
+    gh.check_dispatch(ws, rid, rw, offset, T)
+    npkw = gh.to_numpy_inputs({**kw, "gemm1_weights": w[0][:1], "gemm2_weights": w[2][:1]})
+    npkw["gemm1_weights"], npkw["gemm1_weights_scale"], npkw["gemm2_weights"], npkw["gemm2_weights_scale"] = wnp
+    npkw["dequant_cache"] = _WEIGHTS["cache"]
+    rng = np.random.default_rng(T + offset)
+    tokens = None if T <= 65 else np.sort(rng.choice(T, 24, replace=False))
+    sel = slice(None) if tokens is None else tokens
+    emu = olayer.layer_forward(**npkw, mode="emulated", tokens=tokens, requant_block=_requant_block(T))
+    what = f"T={T} offset={offset}"
+    n = len(emu["sorted_slot"])
+    act, sc = _read_act(ws, n)
+    _check_intermediate(act, sc, emu, _wanted_rows(emu, tokens), what)
+    _check_second_half(got[sel], npkw, act, sc, tokens, what)
+    g, r = got[sel], emu["output"]
+    rel = np.sqrt(np.mean((g - r) ** 2)) / max(np.sqrt(np.mean(r ** 2)), 1e-30)
+    print(f"{what} vs emulated oracle: rel rms {rel:.4g}", flush=True)
+    assert rel <= 0.01
+    assert np.all(got[emu["token_nlocal"] == 0] == 0)
+
+
 def test_layer_last_expert_group():
     """local_expert_offset = 224: the device owns the last routing group."""
     gh = _gh()
