@@ -178,8 +178,9 @@ namespace {
 // The launch sequence of moe_fp8_run; with `events`, events[i] is recorded on the stream
 // before stage i+1 (routing [+ dispatch], GEMM1, requantisation + GEMM2 + combine) and
 // events[3] after the last launch.
-// packed: the packed copy of W13 and W2 (moe_fp8_pack_weights) or null; read only up to 64
-// tokens, where the decode kernels stream it instead of args' weights.
+// packed: the packed copy of W13 and W2 (moe_fp8_pack_weights) or null; read only up to 256
+// tokens (MOE_FP8_PACKED_MAX_TOKENS), where the streaming kernels read it instead of args'
+// weights.
 int run_layer(const moe_fp8_args* args, void* workspace, size_t workspace_bytes, hipStream_t stream,
               hipEvent_t* events, const uint8_t* packed = nullptr) {
   moe_fp8_layout L;
@@ -332,7 +333,12 @@ int moe_fp8_run_static(const moe_fp8_args* args, hipStream_t stream) {
   if (args->num_tokens < 0) return MOE_FP8_EINVAL_TOKENS;
   if (args->num_tokens > MOE_FP8_STATIC_MAX_TOKENS) return MOE_FP8_ESTATIC_TOKENS;
   if (args->num_tokens == 0) return MOE_FP8_OK;
-  int rc = check_device();
+  // every argument check comes before the first call's clear kernel, so that an error other
+  // than MOE_FP8_ELAUNCH never leaves a launch behind (the stand-in pointer is only tested
+  // against null here; run_layer checks again with the real address)
+  moe_fp8_layout L;
+  static uint8_t stand_in;
+  int rc = check_args(args, true, &stand_in, MOE_FP8_STATIC_SCRATCH_BYTES, &L);
   if (rc != MOE_FP8_OK) return rc;
   void* ws = nullptr;
   rc = static_scratch(stream, &ws);

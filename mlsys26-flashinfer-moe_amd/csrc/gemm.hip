@@ -8,10 +8,11 @@
 // work-groups, so that every CU streams about the same number of bytes:
 //   GEMM1: slice = 16 SwiGLU columns = 16 gate rows + the matching 16 up rows of W13[e]
 //          (128 slices); the epilogue writes C = silu(X2) * X1 in fp32 (kernel.py:126-129),
-//          and requant_kernel turns each row's 128-column blocks into e4m3 with
-//          scale = max(amax/448, 1e-12) (kernel.py:131-135 uses 64-column blocks; this
-//          layer uses 128 so that GEMM2 sees one activation scale per K-step).
-//   GEMM2: slice = 64 hidden rows of W2[e] (112 slices); v = acc * routing weight
+//          and requant_kernel turns each row's 64-column blocks into e4m3 with
+//          scale = max(amax/448, 1e-12) (kernel.py:131-135, the reference's 1x64 blocks).
+//   GEMM2: slice = 64 hidden rows of W2[e] (112 slices); each 128-wide K-step carries two
+//          activation scales, one per 64-column half (one MFMA per half, the other half's
+//          activation bytes zeroed); v = acc * routing weight
 //          (kernel.py:236-237); a token with one local assignment gets v written straight
 //          to its output row, the others park v in `partial` by flat slot for
 //          combine_kernel (the reference adds with fp32 atomics, kernel.py:246-250).
@@ -27,6 +28,8 @@
 // [16g, 16g+16) and [64+16g, 64+16g+16) of its row (weights and activations alike, so the
 // dot products are unchanged). Each 16-byte load instruction of a wavefront then reads
 // whole 64-byte segments of 16 rows.
+#include <type_traits>
+
 #include "moe_internal.h"
 #include "moe_device.h"
 
@@ -55,6 +58,12 @@ constexpr int kStreamWaves = 4;                      // wavefronts per work-grou
 // Requantising GEMM1's fp32 rows inside GEMM2 instead of in requant_kernel was measured
 // and is slower (T=64: GEMM2 + combine 68 -> 80 us): the per-element IEEE divisions, four
 // times the activation bytes and fewer resident wavefronts cost more than the launch.
+// Columns per requantisation scale of the GEMM1 output on the streaming path: the
+// reference's 1x64 block (kernel.py:131-135); GEMM2 then applies two activation scales per
+// 128-wide K block.
+constexpr int kQuantCols = 64;
+constexpr int kQuantBlocks = kInter / kQuantCols;    // 32 per row
+
 template <int KIND>
 struct StreamShape;
 template <>
@@ -94,11 +103,13 @@ __device__ __forceinline__ v8i load_frag_packed(const uint8_t* p) {
 constexpr size_t kPackedFrag = 64 * 32;
 constexpr size_t kPackedW13Bytes = (size_t)kExpertsLocal * 2 * kInter * kHidden;
 
-template <int NF, int NG>
+// sa: the activation scale of the lane's row for the K-step: GEMM1 one (1x128 hidden
+// scales), GEMM2 two (the 1x64 scales of the K-step's two halves).
+template <int NF, int NG, typename SA>
 struct StreamStage {
   v8i w[NF];
   v8i a[NG];
-  float sa[NG];
+  SA sa[NG];
 };
 
 // The accumulators of one work unit for an item of NG row groups (NG <= 2). Every K-step
@@ -117,6 +128,8 @@ __device__ __forceinline__ void stream_accumulate(const GemmParams& p, int e, in
   constexpr int NF = S::kFrags;
   constexpr int NB = S::kRing;
   constexpr int KMAIN = KS - KS % NB;   // steps of the ring-unrolled main loop
+  using SA = typename std::conditional<KIND == kG1, float, float2>::type;
+  using Stage = StreamStage<NF, NG, SA>;
 
   // weight fragments and their block-scale rows; lane k of sw_lane[f] holds the scale of
   // K-step k
@@ -151,7 +164,7 @@ __device__ __forceinline__ void stream_accumulate(const GemmParams& p, int e, in
   // (packed W13 interleaves the gate and up fragments of a K-step)
   constexpr size_t kWStep = PACKED ? (KIND == kG1 ? 2 : 1) * kPackedFrag : 128;
   auto wload = [&](const uint8_t* q) { return PACKED ? load_frag_packed(q) : load_frag(q); };
-  StreamStage<NF, NG> ring[NB];
+  Stage ring[NB];
   // the weight loads of the first steps go out before the activation addresses are known
   // (GEMM1 reads them from sorted_token, one more memory round trip)
 #pragma unroll
@@ -173,19 +186,19 @@ __device__ __forceinline__ void stream_accumulate(const GemmParams& p, int e, in
       sap[g] = p.hidden_scale + tok;
     } else {
       ap[g] = p.act + (size_t)(r0 + mm) * kInter + (lane >> 4) * 16;
-      sap[g] = p.act_scale + (size_t)(r0 + mm) * kIBlocks;
+      sap[g] = p.act_scale + (size_t)(r0 + mm) * kQuantBlocks;
     }
   }
-  const size_t sa_stride = (KIND == kG1) ? (size_t)p.T : 1;
 
-  auto issue_a = [&](int k, StreamStage<NF, NG>& st) {
+  auto issue_a = [&](int k, Stage& st) {
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
       st.a[g] = load_frag(ap[g] + k * 128);
-      st.sa[g] = sap[g][k * sa_stride];
+      if constexpr (KIND == kG1) st.sa[g] = sap[g][(size_t)k * p.T];   // hidden scales [56, T]
+      else st.sa[g] = *reinterpret_cast<const float2*>(sap[g] + 2 * k);
     }
   };
-  auto issue = [&](int k, StreamStage<NF, NG>& st) {
+  auto issue = [&](int k, Stage& st) {
 #pragma unroll
     for (int f = 0; f < NF; ++f) st.w[f] = wload(wf[f] + k * kWStep);
     issue_a(k, st);
@@ -204,17 +217,33 @@ __device__ __forceinline__ void stream_accumulate(const GemmParams& p, int e, in
     // keep each step's loads ahead of its math (the scheduler would otherwise pull later
     // steps' MFMAs above these loads and shrink the ring to one step in flight)
     __builtin_amdgcn_sched_barrier(0);
-    const StreamStage<NF, NG>& st = ring[u];
+    const Stage& st = ring[u];
     float sc[NF];
 #pragma unroll
     for (int f = 0; f < NF; ++f) sc[f] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sw_lane[f]), k));
 #pragma unroll
-    for (int g = 0; g < NG; ++g)
+    for (int g = 0; g < NG; ++g) {
+      if constexpr (KIND == kG1) {
 #pragma unroll
-      for (int f = 0; f < NF; ++f) {
-        const v4f d = mfma16x16x128_fp8(st.w[f], st.a[g], zero);
-        acc[f][g] += d * (st.sa[g] * sc[f]);
+        for (int f = 0; f < NF; ++f) {
+          const v4f d = mfma16x16x128_fp8(st.w[f], st.a[g], zero);
+          acc[f][g] += d * (st.sa[g] * sc[f]);
+        }
+      } else {
+        // the two 64-column halves of the K-step (lanes hold bytes [16j, 16j+16) of the first
+        // half in a[0..3] and of the second in a[4..7]), each with its own scale
+        const v4i kZero4 = {0, 0, 0, 0};
+        const v8i a_lo = join(lo_half(st.a[g]), kZero4);
+        const v8i a_hi = join(kZero4, hi_half(st.a[g]));
+#pragma unroll
+        for (int f = 0; f < NF; ++f) {
+          const v4f d_lo = mfma16x16x128_fp8(st.w[f], a_lo, zero);
+          const v4f d_hi = mfma16x16x128_fp8(st.w[f], a_hi, zero);
+          acc[f][g] += d_lo * (st.sa[g].x * sc[f]);
+          acc[f][g] += d_hi * (st.sa[g].y * sc[f]);
+        }
       }
+    }
     __builtin_amdgcn_sched_barrier(0);
   };
 #pragma nounroll
@@ -303,11 +332,6 @@ __global__ __launch_bounds__(kStreamWaves * 64) void gemm_stream_kernel(GemmPara
   const int n_items = min(p.counters[kCtrItems], p.max_items);
   stream_units<KIND, MAXNG, PACKED>(p, n_items, reinterpret_cast<const int4*>(p.work_items), p.sorted_token);
 }
-
-// Columns per requantisation scale of 16-row items: the reference's 1x64 block
-// (kernel.py:131-135); GEMM2 then applies two activation scales per 128-wide K block.
-constexpr int kQuantCols = 64;
-constexpr int kQuantBlocks = kInter / kQuantCols;    // 32 per row
 
 // Decode batches of up to kFusedDispatchTokens tokens: GEMM1 without a dispatch launch before
 // it. Every work-group rebuilds the call's dispatch from the top-k lists in LDS, the same as
@@ -791,9 +815,11 @@ hipError_t launch_gemm1(const GemmParams& p, int rows_per_item, bool packed, hip
 }
 
 hipError_t launch_gemm1_dispatch(const GemmParams& p, const RouteParams& rp, bool packed, hipStream_t s) {
-  static int occ = 0;
+  // one wave of resident work-groups of the instance launched (each has its own occupancy)
+  static int occ_rows = 0, occ_packed = 0;
   if (p.T <= 0 || p.T > kFusedDispatchTokens || rp.rows_per_item != kFusedItemRows) return hipErrorInvalidValue;
-  int grid = num_cus() * resident_per_cu(gemm1_stream_dispatch_kernel<false>, occ);
+  int grid = num_cus() * (packed ? resident_per_cu(gemm1_stream_dispatch_kernel<true>, occ_packed)
+                                 : resident_per_cu(gemm1_stream_dispatch_kernel<false>, occ_rows));
   const int cap = (kFusedItems * StreamShape<kG1>::kSlices + kStreamWaves - 1) / kStreamWaves;
   if (grid > cap) grid = cap;
   if (packed)
@@ -808,10 +834,9 @@ hipError_t launch_requant(const GemmParams& p, int rows_per_item, hipStream_t s)
   int grid = p.T * kTopK;                      // rows of the SwiGLU buffer
   if (grid > num_cus() * 8) grid = num_cus() * 8;
   if (grid <= 0) return hipSuccess;
-  if (requant_block_for(rows_per_item) == kQuantCols)
-    hipLaunchKernelGGL(requant_kernel<kQuantCols>, dim3(grid), dim3(256), 0, s, p);
-  else
-    hipLaunchKernelGGL(requant_kernel<128>, dim3(grid), dim3(256), 0, s, p);
+  static_assert(kQuantCols == 64, "the streaming path requantises per 64 columns");
+  if (requant_block_for(rows_per_item) != kQuantCols) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(requant_kernel<kQuantCols>, dim3(grid), dim3(256), 0, s, p);
   return hipGetLastError();
 }
 

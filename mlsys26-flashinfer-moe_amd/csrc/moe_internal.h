@@ -77,8 +77,9 @@ inline int rows_per_item_for(int T) {
 }
 
 // Columns per requantisation scale of the GEMM1 output: the reference's 64 (kernel.py:131-135)
-// for 16-row items, 128 otherwise (one activation scale per 128-wide K block of GEMM2).
-inline int requant_block_for(int rows_per_item) { return rows_per_item == 16 ? 64 : 128; }
+// on the streaming path (items of up to 32 rows, up to 256 tokens), 128 on the tile path (one
+// activation scale per 128-wide K block of the tile GEMM2).
+inline int requant_block_for(int rows_per_item) { return rows_per_item <= 32 ? 64 : 128; }
 
 int compute_layout(int32_t T, moe_fp8_layout* out);
 

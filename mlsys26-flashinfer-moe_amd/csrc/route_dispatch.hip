@@ -177,9 +177,12 @@ __device__ __forceinline__ int route_wave(const RouteParams& p, const float* s_b
     key = max_u64(key, dpp_u64<kDppMirror>(key));
     const int e = key_index(key);
     my_id = (r == k) ? e : my_id;
+    // the winner's score becomes -inf (kernel.py:534), not less: once fewer than 8 finite
+    // scores remain, every -inf entry ties, the chosen ones included, and the lowest index
+    // wins again (a token can then name one expert several times, as the reference does)
     const uint32_t drop = ((e >> 4) == r) ? (uint32_t)(e & 15) : 16u;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) c[i] = (drop == (uint32_t)i) ? 0u : c[i];
+    for (int i = 0; i < 16; ++i) c[i] = (drop == (uint32_t)i) ? kOrderedNegInf : c[i];
   }
   // Weights from the unbiased scores, renormalised in selection order and scaled
   // (kernel.py:537-538): w = s / (s_0 + ... + s_7 + 1e-20) * rsf. Lane r < 8 recomputes
@@ -267,9 +270,10 @@ __device__ __forceinline__ int route_wide(const RouteParams& p, const float* s_b
     const uint32_t klo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)key, 63);
     const int e = key_index((uint64_t)klo);
     my_id = (lane == k) ? e : my_id;
+    // the winner drops to -inf, where it ties with the other -inf entries (kernel.py:534)
     const uint32_t drop = ((e >> 2) == lane) ? (uint32_t)(e & 3) : 4u;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) c[i] = (drop == (uint32_t)i) ? 0u : c[i];
+    for (int i = 0; i < 4; ++i) c[i] = (drop == (uint32_t)i) ? kOrderedNegInf : c[i];
   }
   // weights (kernel.py:537-538), as route_wave: w = s / (s_0 + ... + s_7 + 1e-20) * rsf
   const float sv = (lane < kTopK) ? sigmoid_f32(p.logits[(size_t)t * kExpertsGlobal + my_id]) : 0.0f;

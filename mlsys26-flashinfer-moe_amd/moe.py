@@ -163,13 +163,19 @@ class PackedWeightCache:
     used is never freed (a stale one moves to a retired list), because the graph holds its
     address. A copy handed to a stream other than the one that built it is recorded on that
     stream (Tensor.record_stream), so that dropping a stale copy never lets the allocator reuse
-    its memory while work queued on that stream may still read it. `make(w13, w2)`,
-    `capturing()`, `stream_id()` and `record(packed)` are injectable so that the policy is
-    testable without a GPU.
+    its memory while work queued on that stream may still read it, and that stream first waits
+    for the event recorded right after the packing kernel: callers only read the weights and
+    cannot know that a copy exists, so nothing else would order their stream after the build
+    (under capture no wait is added: torch.cuda.graph synchronises the device before capturing,
+    and a capture cannot wait on an event recorded outside it). A weight set whose copy does not
+    fit in device memory (the allocation raises torch.cuda.OutOfMemoryError) runs on the
+    row-major weights, and its copy is not tried again until clear(). `make(w13, w2)`,
+    `capturing()`, `stream_id()`, `record(packed)`, `event()` (an event recorded on the current
+    stream) and `wait(event)` are injectable so that the policy is testable without a GPU.
     """
 
     def __init__(self, max_sets: int = 4, make=None, capturing=None, storage_ref=None, stream_id=None,
-                 record=None):
+                 record=None, event=None, wait=None):
         from torch.multiprocessing.reductions import StorageWeakRef
         self.max_sets = max_sets
         self._make = make or (lambda w13, w2: pack_weights(w13, w2))
@@ -177,9 +183,12 @@ class PackedWeightCache:
         self._ref = storage_ref or (lambda t: StorageWeakRef(t.untyped_storage()))
         self._stream_id = stream_id or (lambda: torch.cuda.current_stream().cuda_stream)
         self._record = record or (lambda packed: packed.record_stream(torch.cuda.current_stream(packed.device)))
+        self._event = event or _record_event
+        self._wait = wait or (lambda ev: torch.cuda.current_stream().wait_event(ev))
         self._lock = threading.Lock()
         self._entries = {}
         self._retired = []
+        self._failed = set()   # weight sets whose copy did not fit in device memory
 
     def get(self, w13: torch.Tensor, w2: torch.Tensor):
         """The packed copy for (w13, w2), built if missing or stale; None when the set does
@@ -197,9 +206,11 @@ class PackedWeightCache:
                 ent["captured"] = ent["captured"] or capturing
                 if stream not in ent["streams"]:
                     self._record(ent["packed"])
+                    if not capturing:
+                        self._wait(ent["event"])   # the packing kernel before this stream's reads
                     ent["streams"].add(stream)
                 return ent["packed"]
-            if capturing:
+            if capturing or (key, version) in self._failed:
                 return None
             if ent is not None:
                 self._drop(key)
@@ -207,9 +218,13 @@ class PackedWeightCache:
                 self._drop(k)
             if len(self._entries) >= self.max_sets:
                 return None
-            packed = self._make(w13, w2)
+            try:
+                packed = self._make(w13, w2)
+            except torch.cuda.OutOfMemoryError:
+                self._failed.add((key, version))
+                return None
             self._entries[key] = dict(ref13=self._ref(w13), ref2=self._ref(w2), version=version, packed=packed,
-                                      captured=False, streams={stream})
+                                      captured=False, streams={stream}, event=self._event())
             return packed
 
     def _drop(self, key):
@@ -222,6 +237,7 @@ class PackedWeightCache:
         with self._lock:
             for k in list(self._entries):
                 self._drop(k)
+            self._failed.clear()
 
     def __len__(self) -> int:
         return len(self._entries)
@@ -229,6 +245,13 @@ class PackedWeightCache:
     @property
     def retired(self) -> list:
         return list(self._retired)
+
+
+def _record_event():
+    """An event recorded on the current stream (after the work queued there so far)."""
+    ev = torch.cuda.Event()
+    ev.record()
+    return ev
 
 
 _packed_weights = PackedWeightCache()

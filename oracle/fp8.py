@@ -47,11 +47,6 @@ def encode(x: np.ndarray) -> np.ndarray:
     return (code | sign).astype(np.uint8)
 
 
-def quantize(x: np.ndarray) -> np.ndarray:
-    """Round float32 values to the nearest e4m3fn values (as float32)."""
-    return decode(encode(x))
-
-
 def bf16_bits(x: np.ndarray) -> np.ndarray:
     """float32 -> bf16 bit patterns (uint16), round to nearest even, NaN -> quiet NaN."""
     u = np.asarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)

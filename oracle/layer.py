@@ -120,7 +120,9 @@ def layer_forward(routing_logits, routing_bias, hidden_states, hidden_states_sca
             lo, hi = int(d["expert_start"][e]), int(d["expert_start"][e + 1])
             rows = np.arange(lo, hi)
             rows = rows[done[rows]]
-            out[pos[d["sorted_token"][rows]]] += y[rows]
+            # a token that names expert e more than once (kernel.py:522-534 can repeat an id)
+            # has several rows here: add each of them, in bucket (slot) order
+            np.add.at(out, pos[d["sorted_token"][rows]], y[rows])
     return {
         "topk_ids": ids,
         "topk_weights": wts,

@@ -50,11 +50,12 @@ def test_layout_consistent(pkg, T):
     assert L.route_blocks == (T + 15) // 16
     assert L.max_work_items == 32 + (8 * T + L.rows_per_item - 1) // L.rows_per_item
     assert L.counters == 0
-    # up to 64 tokens (16-row items) the requantisation is per 64 columns and GEMM2 combines in
-    # LDS (no parked rows); items of up to 32 rows keep GEMM1's fp32 SwiGLU rows
+    # up to 64 tokens (16-row items) GEMM2 combines in LDS (no parked rows); items of up to 32
+    # rows (up to 256 tokens) keep GEMM1's fp32 SwiGLU rows and requantise per 64 columns, the
+    # reference's block; the tile path per 128
     decode = L.rows_per_item == 16
     assert L.rows_per_item == (16 if T <= 64 else 32 if T <= 256 else L.rows_per_item)
-    assert L.requant_block == (64 if decode else 128)
+    assert L.requant_block == (64 if L.rows_per_item <= 32 else 128)
     arrays = [
         ("topk_ids", 4 * 8 * T), ("topk_weights", 4 * 8 * T), ("expert_count", 4 * 32),
         ("expert_start", 4 * 33), ("sorted_token", 4 * 8 * T), ("sorted_weight", 4 * 8 * T),
@@ -184,3 +185,32 @@ def test_quantize_hidden_argument_errors(pkg, lib):
     import torch
     if not torch.cuda.is_available():
         assert f(0x1000, L.HIDDEN_BF16, 4, 0x2000, 0x3000, None) == L.EDEVICE
+
+
+def test_static_entry_reports_argument_errors_first(pkg, lib):
+    """moe_fp8_run_static checks every argument before its first call on a device queues the
+    clear kernel of its built-in workspace: null pointers, bad dtypes and oversize batches come
+    back as their codes with no device at hand (the GPU tests cover the device path)."""
+    L = pkg._lib
+    f = lib.moe_fp8_run_static
+    assert f(None, None) == L.EINVAL_POINTER
+    a = _args(pkg)
+    a.gemm2_weights_scale = None
+    assert f(ctypes.byref(a), None) == L.EINVAL_POINTER
+    a = _args(pkg)
+    a.routing_logits = None
+    assert f(ctypes.byref(a), None) == L.EINVAL_POINTER
+    a = _args(pkg)
+    a.routing_bias_dtype = 7
+    assert f(ctypes.byref(a), None) == L.EINVAL_BIAS_DTYPE
+    a = _args(pkg)
+    a.output_dtype = 5
+    assert f(ctypes.byref(a), None) == L.EINVAL_OUT_DTYPE
+    a = _args(pkg, L.STATIC_MAX_TOKENS + 1)
+    assert f(ctypes.byref(a), None) == L.ESTATIC_TOKENS
+    a = _args(pkg, -2)
+    assert f(ctypes.byref(a), None) == L.EINVAL_TOKENS
+    assert f(ctypes.byref(_args(pkg, 0)), None) == L.OK
+    import torch
+    if not torch.cuda.is_available():
+        assert f(ctypes.byref(_args(pkg)), None) == L.EDEVICE

@@ -104,7 +104,7 @@ def _run_full(kw, out_dtype=torch.bfloat16):
 def _requant_block(T):
     """Columns per activation scale of the layer at T tokens, from the library's layout."""
     rb = int(_gh()._lib.workspace_layout(T).requant_block)
-    assert rb == (64 if T <= 64 else 128)
+    assert rb == (64 if T <= 256 else 128)
     return rb
 
 
@@ -548,3 +548,58 @@ def test_zero_tokens():
     out = torch.empty((0, 7168), dtype=torch.bfloat16, device=dev)
     assert gh.pkg.run(**kw, output=out) is None
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("T", [16, 64, 100, 300])
+def test_layer_with_a_repeated_expert_from_routing(T):
+    """Router biases of -inf on all but experts 3, 17, 40, 70 and 100: fewer than 8 finite
+    scores remain in the kept groups, so every token's last three top-k slots name expert 0
+    (kernel.py:522-534). With local experts 0-31 each token then has five local assignments,
+    three of them to expert 0, whose weighted rows all add to its output. Run through
+    moe_fp8_run at T=16 and 64 (dispatch rebuilt in GEMM1, combine in GEMM2), 100 (32-row
+    streaming items) and 300 (tile GEMMs, parked rows and the combine)."""
+    gh = _gh()
+    dev = torch.device("cuda:0")
+    w, wnp = _weights()
+    print(f"repeated expert from routing T={T}", flush=True)
+    logits, _, hq, hs = gh.inputs.make_activations(T, 6100 + T, dev)
+    bias_np = np.full(256, -np.inf, np.float32)
+    bias_np[[3, 17, 40, 70, 100]] = np.random.default_rng(T).standard_normal(5).astype(np.float32) * 0.1
+    bias = torch.from_numpy(bias_np).to(torch.bfloat16).to(dev)
+    rsf = gh.inputs.ROUTED_SCALING_FACTOR
+    kw = dict(routing_logits=logits, routing_bias=bias, hidden_states=hq, hidden_states_scale=hs,
+              gemm1_weights=w[0], gemm1_weights_scale=w[1], gemm2_weights=w[2], gemm2_weights_scale=w[3],
+              local_expert_offset=0, routed_scaling_factor=rsf)
+    out = torch.full((T, 7168), float("nan"), dtype=torch.bfloat16, device=dev)
+    ws = gh.new_workspace(T, dev)
+    gh.run_layer(gh.make_args(**kw, output=out), ws)
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    assert np.isfinite(got).all()
+    ids = gh.read(ws, "topk_ids", torch.int32, T * 8).reshape(T, 8)
+    wts = gh.read(ws, "topk_weights", torch.float32, T * 8).reshape(T, 8)
+    rid, rw = orouting.route(logits.cpu().numpy(), bias.float().cpu().numpy(), rsf)
+    assert np.all(rid[:, 5:] == 0) and np.all(np.sort(rid[:, :5], axis=1) == [3, 17, 40, 70, 100])
+    assert np.array_equal(ids, rid)
+    assert np.array_equal(wts.view(np.uint32), rw.view(np.uint32))
+    gh.check_dispatch(ws, rid, rw, 0, T)
+    npkw = gh.to_numpy_inputs({**kw, "gemm1_weights": w[0][:1], "gemm2_weights": w[2][:1]})
+    npkw["gemm1_weights"], npkw["gemm1_weights_scale"], npkw["gemm2_weights"], npkw["gemm2_weights_scale"] = wnp
+    npkw["dequant_cache"] = _WEIGHTS["cache"]
+    tokens = None if T <= 100 else np.sort(np.random.default_rng(T).choice(T, 24, replace=False))
+    sel = slice(None) if tokens is None else tokens
+    emu = olayer.layer_forward(**npkw, mode="emulated", tokens=tokens, requant_block=_requant_block(T))
+    assert np.all(emu["token_nlocal"] == 5)
+    what = f"repeated expert T={T}"
+    n = len(emu["sorted_slot"])
+    act, sc = _read_act(ws, n)
+    _check_intermediate(act, sc, emu, _wanted_rows(emu, tokens), what)
+    _check_second_half(got[sel], npkw, act, sc, tokens, what)
+    g, r = got[sel], emu["output"]
+    rel = np.sqrt(np.mean((g - r) ** 2)) / max(np.sqrt(np.mean(r ** 2)), 1e-30)
+    print(f"{what} vs emulated oracle: rel rms {rel:.4g}", flush=True)
+    assert rel <= 0.01
+    ref = olayer.layer_forward(**npkw, mode="definition", tokens=tokens)["output"]
+    rel = np.sqrt(np.mean((g - ref) ** 2)) / max(np.sqrt(np.mean(ref ** 2)), 1e-30)
+    print(f"{what} vs definition: rel rms {rel:.4g}", flush=True)
+    assert rel <= 0.05

@@ -148,7 +148,9 @@ def test_run_keeps_a_packed_copy_per_weight_set():
 
 def test_run_on_a_second_stream_uses_the_copy():
     """run() on a side stream with a copy built on another: the copy is recorded on the side stream
-    (Tensor.record_stream) and the result is the row-major one, bit for bit."""
+    (Tensor.record_stream), the side stream waits for the packing kernel through the cache's event
+    (nothing else orders it: the inputs are ready before the first call and the side stream does
+    not wait for the building stream), and the result is the row-major one, bit for bit."""
     gh = _gh()
     moe = gh.pkg.moe
     dev = torch.device("cuda:0")
@@ -165,10 +167,10 @@ def test_run_on_a_second_stream_uses_the_copy():
     moe._packed_weights = cache
     try:
         out = torch.empty_like(ref)
-        gh.pkg.run(**kw, output=out)                      # builds the copy on the current stream
-        side = torch.cuda.Stream(device=dev)
-        side.wait_stream(torch.cuda.current_stream(dev))
         out2 = torch.empty_like(ref)
+        side = torch.cuda.Stream(device=dev)
+        torch.cuda.synchronize()                          # inputs, ref and outputs are ready
+        gh.pkg.run(**kw, output=out)                      # builds the copy on the current stream
         with torch.cuda.stream(side):
             gh.pkg.run(**kw, output=out2)
         torch.cuda.current_stream(dev).wait_stream(side)

@@ -184,3 +184,36 @@ def test_workspace_reuse_across_calls():
         gh.route_dispatch(args, ws)
         rid, rw = orouting.route(logits, bias, 2.5)
         gh.check_dispatch(ws, rid, rw, off, T)
+
+
+FEW_FINITE = {
+    0: [],
+    1: [77],
+    5: [3, 17, 40, 70, 100],
+    7: [0, 1, 2, 33, 34, 64, 96],
+    "mixed": [0, 1, 32, 64, 96, 128, 129, 160, 192, 193, 224],
+}
+
+
+@pytest.mark.parametrize("T", [37, 300])
+@pytest.mark.parametrize("case", list(FEW_FINITE))
+def test_routing_fewer_than_top_k_finite_candidates(case, T):
+    """Biases of -inf leave 0, 1, 5 or 7 finite biased scores in the kept groups (and 7 in a
+    mix of finite and -inf group scores). As in kernel.py:522-534, the remaining top-k slots
+    all name expert 0 (the first index of the -inf maximum, a chosen expert included), and the
+    weights count each repeat. T=37 runs route_wide_kernel, T=300 route_kernel; both bias
+    dtypes that can hold -inf in storage of their own are used (fp32, bf16)."""
+    rng = np.random.default_rng(57 + T)
+    logits = rng.standard_normal((T, 256)).astype(np.float32)
+    bias = np.full(256, -np.inf, np.float32)
+    fin = FEW_FINITE[case]
+    bias[fin] = (rng.standard_normal(len(fin)) * 0.1).astype(np.float32)
+    for bias_dtype in (torch.float32, torch.bfloat16):
+        ws, gh = _route_gpu(logits, bias, offset=0, bias_dtype=bias_dtype)
+        bias_cast = torch.from_numpy(bias).to(bias_dtype).float().numpy()
+        rid, rw = orouting.route(logits, bias_cast, 2.5)
+        assert np.all(rid[:, -1] == 0), "the last slot repeats expert 0"
+        assert np.array_equal(gh.read(ws, "topk_ids", torch.int32, T * 8).reshape(T, 8), rid)
+        assert np.array_equal(gh.read(ws, "topk_weights", torch.float32, T * 8).reshape(T, 8).view(np.uint32),
+                              rw.view(np.uint32))
+        gh.check_dispatch(ws, rid, rw, 0, T)

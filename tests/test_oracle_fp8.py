@@ -52,3 +52,14 @@ def test_bf16_rounding_matches_torch():
     # ties to even, closed form
     x = np.array([0x3F808000, 0x3F818000], dtype=np.uint32).view(np.float32)
     assert list(fp8.bf16_bits(x)) == [0x3F80, 0x3F82]
+
+
+def test_bf16_to_f32_matches_torch():
+    """Every bf16 bit pattern widens to torch's CPU bfloat16 -> float32 value (NaNs as NaN)."""
+    import torch
+    bits = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    got = fp8.bf16_to_f32(bits)
+    exp = torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16).float().numpy()
+    nan = np.isnan(exp)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), exp[~nan].view(np.uint32))

@@ -138,3 +138,22 @@ def test_act_override_reproduces_emulated_mode(requant_block):
     assert diff[tok] and diff.sum() == 1
     with pytest.raises(ValueError):
         olayer.layer_forward(**kw, mode="definition", topk=topk, act_override=(act, sc))
+
+
+@pytest.mark.parametrize("mode", ["definition", "emulated"])
+def test_repeated_expert_in_one_token(mode):
+    """A token may name one local expert several times (kernel.py:522-534 repeats expert 0 once
+    fewer than 8 finite scores remain); each slot's weighted row is added, as the reference's
+    per-slot scatter (kernel.py:313-321) and atomic add (kernel.py:246-250) do."""
+    kw, (ids, w) = _inputs(3, 6)
+    ids[0] = [OFF + 1, OFF + 3, 100, 101, 102, OFF, OFF, OFF]
+    ids[2, :3] = [OFF + 2, OFF + 2, 50]
+    r = olayer.layer_forward(**kw, mode=mode, topk=(ids, w), requant_block=64)
+    ref = _brute(kw, (ids, w), requant_block=64 if mode == "emulated" else None)
+    scale = np.abs(ref).max()
+    err = np.abs(r["output_f32"] - ref)
+    if mode == "definition":
+        np.testing.assert_allclose(r["output_f32"], ref, rtol=1e-4, atol=1e-5 * scale)
+    else:
+        assert np.mean(err > 1e-3 * scale) < 0.01 and err.max() < 0.05 * scale
+    assert r["token_nlocal"][0] == 5 and r["token_nlocal"][2] >= 2

@@ -2,6 +2,8 @@
 DeepseekV3TopkRouter (golden fixture), invariants and closed-form special cases."""
 from pathlib import Path
 
+import math
+
 import numpy as np
 import pytest
 
@@ -120,3 +122,88 @@ def test_weights_use_unbiased_scores():
     # weight ratio equals the ratio of unbiased scores
     s = 1.0 / (1.0 + np.exp(-np.arange(8.0)))
     np.testing.assert_allclose([d1[e] / d1[0] for e in range(8)], s / s[0], rtol=1e-6)
+
+
+def _brute_topk(b_row, kept_groups, top_k=8, gsz=32):
+    """kernel.py:515-534 as plain Python loops over one token: -inf outside the kept groups;
+    each round scans all experts for the largest value, keeps the first index holding it,
+    then sets that entry to -inf (so a chosen expert ties with every other -inf entry)."""
+    pruned = [float(b_row[e]) if (e // gsz) in kept_groups else -math.inf for e in range(len(b_row))]
+    ids = []
+    for _ in range(top_k):
+        best, arg = -math.inf, None
+        for e, v in enumerate(pruned):
+            if arg is None or v > best:
+                best, arg = v, e
+        ids.append(arg)
+        pruned[arg] = -math.inf
+    return ids
+
+
+def _brute_groups(b_row, topk_group=4, n_group=8, gsz=32):
+    """kernel.py:479-501 as loops: group score = max + max of the rest (first maximum masked);
+    rounds of 'largest score among unselected groups, lowest index on ties'."""
+    scores = []
+    for g in range(n_group):
+        vals = [float(v) for v in b_row[g * gsz:(g + 1) * gsz]]
+        i1 = max(range(gsz), key=lambda i: (vals[i], -i))
+        rest = [v for i, v in enumerate(vals) if i != i1]
+        scores.append(np.float32(vals[i1]) + np.float32(max(rest)))
+    kept = []
+    for _ in range(topk_group):
+        cand = [g for g in range(n_group) if g not in kept]
+        kept.append(max(cand, key=lambda g: (scores[g], -g)))
+    return set(kept)
+
+
+FEW_FINITE = {
+    0: [],
+    1: [77],
+    5: [3, 17, 40, 70, 100],
+    7: [0, 1, 2, 33, 34, 64, 96],
+    "mixed": [0, 1, 32, 64, 96, 128, 129, 160, 192, 193, 224],
+}
+
+
+@pytest.mark.parametrize("case", list(FEW_FINITE))
+def test_route_fewer_than_top_k_finite_candidates(case):
+    """Biases of -inf leave fewer than 8 finite biased scores in the kept groups. Then, as in
+    kernel.py:522-534, the maximum of a later round is -inf and its first index, expert 0, wins,
+    again in every later round: a token names one expert several times. Pinned by the loop restatement above and by closed forms."""
+    rng = np.random.default_rng(31)
+    logits = rng.standard_normal((40, 256)).astype(np.float32)
+    bias = np.full(256, -np.inf, np.float32)
+    fin = FEW_FINITE[case]
+    bias[fin] = (rng.standard_normal(len(fin)) * 0.1).astype(np.float32)
+    ids, w = routing.route(logits, bias, 2.5)
+    b = routing.sigmoid_f32(logits) + bias
+    s = routing.sigmoid_f32(logits)
+    for t in range(logits.shape[0]):
+        kept = _brute_groups(b[t])
+        assert ids[t].tolist() == _brute_topk(b[t], kept)
+        nfin = sum(1 for e in fin if e // 32 in kept)
+        assert nfin < 8
+        # closed form: the finite candidates first (descending b, lower index on ties), then
+        # expert 0 in every remaining slot: by then every entry is -inf and 0 is the first index
+        first = sorted((e for e in fin if e // 32 in kept), key=lambda e: (-b[t, e], e))
+        assert ids[t, :nfin].tolist() == first
+        assert ids[t, nfin:].tolist() == [0] * (8 - nfin)
+        # weights: unbiased scores of the named experts, repeats included, over their sum
+        sv = s[t, ids[t]].astype(np.float64)
+        np.testing.assert_allclose(w[t], sv / sv.sum() * 2.5, rtol=3e-6)
+    if case == 0:
+        # all biased scores -inf: groups 0-3 kept, expert 0 eight times, weight rsf/8 at logit 0
+        ids0, w0 = routing.route(np.zeros((2, 256), np.float32), bias, 2.5)
+        assert ids0.tolist() == [[0] * 8] * 2
+        assert np.all(w0 == np.float32(2.5 / 8))
+
+
+def test_route_few_finite_repeats_are_lowest_index_of_kept_groups():
+    """One finite expert (77, group 2): every group score is -inf (a group needs two finite
+    entries), so groups 0-3 are kept on the lowest-index rule, and the seven remaining slots
+    all name expert 0."""
+    bias = np.full(256, -np.inf, np.float32)
+    bias[77] = 0.0
+    logits = np.random.default_rng(2).standard_normal((5, 256)).astype(np.float32)
+    ids, _ = routing.route(logits, bias, 1.0)
+    assert ids.tolist() == [[77] + [0] * 7] * 5

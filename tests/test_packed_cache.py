@@ -29,8 +29,17 @@ class Recorder:
 def _cache(moe, rec, max_sets=2):
     rec.stream = 1
     rec.recorded = []
+    rec.events = []
+    rec.waited = []
+
+    def event():
+        ev = ("event", len(rec.events), rec.stream)   # an event recorded on the current stream
+        rec.events.append(ev)
+        return ev
+
     return moe.PackedWeightCache(max_sets=max_sets, make=rec.make, capturing=lambda: rec.capturing,
-                                 stream_id=lambda: rec.stream, record=lambda p: rec.recorded.append((p, rec.stream)))
+                                 stream_id=lambda: rec.stream, record=lambda p: rec.recorded.append((p, rec.stream)),
+                                 event=event, wait=lambda ev: rec.waited.append((ev, rec.stream)))
 
 
 def _set():
@@ -126,3 +135,50 @@ def test_other_streams_are_recorded_once(moe):
     assert q is not p and rec.recorded == [(p, 2)]
     rec.stream = 1
     assert c.get(w13, w2) is q and rec.recorded == [(p, 2), (q, 1)]
+
+
+def test_other_streams_wait_for_the_build_once(moe):
+    """The packing kernel runs on the building stream. A stream that later reads the copy first
+    waits for the event recorded right after that kernel (once per stream and copy), so that its
+    GEMMs never read the copy before it is written; under capture no wait is added."""
+    rec = Recorder()
+    c = _cache(moe, rec)
+    w13, w2 = _set()
+    p = c.get(w13, w2)
+    assert rec.events == [("event", 0, 1)] and rec.waited == []
+    assert c.get(w13, w2) is p and rec.waited == []          # the building stream is ordered already
+    rec.stream = 2
+    assert c.get(w13, w2) is p and rec.waited == [(("event", 0, 1), 2)]
+    c.get(w13, w2)
+    rec.stream = 1
+    c.get(w13, w2)
+    assert rec.waited == [(("event", 0, 1), 2)]
+    rec.stream, rec.capturing = 3, True
+    assert c.get(w13, w2) is p and rec.waited == [(("event", 0, 1), 2)]
+    assert rec.recorded == [(p, 2), (p, 3)]
+    # a rebuilt copy has its own event, waited for by the other streams again
+    rec.capturing = False
+    w13.add_(1)
+    q = c.get(w13, w2)
+    rec.stream = 2
+    assert c.get(w13, w2) is q and rec.waited[-1] == (rec.events[-1], 2) and len(rec.events) == 2
+
+
+def test_a_copy_that_does_not_fit_runs_row_major(moe):
+    """An out-of-memory error while allocating the copy leaves run() on the row-major weights
+    (no extra memory); the set is not tried again until clear()."""
+    rec = Recorder()
+    calls = []
+
+    def make(w13, w2):
+        calls.append(1)
+        raise torch.cuda.OutOfMemoryError("no room for the packed copy")
+
+    c = _cache(moe, rec)
+    c._make = make
+    w13, w2 = _set()
+    assert c.get(w13, w2) is None and c.get(w13, w2) is None
+    assert len(calls) == 1 and len(c) == 0 and rec.events == []
+    c.clear()
+    c._make = rec.make
+    assert c.get(w13, w2) is rec.built[0]
