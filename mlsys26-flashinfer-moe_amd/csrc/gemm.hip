@@ -255,6 +255,140 @@ __device__ __forceinline__ void stream_accumulate(const GemmParams& p, int e, in
   for (int u = 0; u < KS - KMAIN; ++u) step(KMAIN + u, u);
 }
 
+// Row-major W13 through a wavefront-private LDS ring (GEMM1 units on the caller's row-major
+// weights). A 16-lane pass of a row-major fragment load touches 16 cache lines (one 16-byte
+// piece of each of 16 rows), four times the lines of a pass over the packed copy, and with
+// every wavefront slot streaming the CU's address path is what limits the rate. Here each
+// global_load_lds instruction moves 8 whole 128-byte rows (a 16-lane pass covers 2 lines)
+// and ds_read_b128 gathers the MFMA fragments from the ring. A unit's 32 weight rows of a
+// K-step (the 16 gate rows, then the 16 up rows) are 4 KB, 4 DMA instructions; chunk c of
+// row m sits at m * 128 + 16 * (c ^ ((m >> 1) & 7)), so that the 16 rows of a ds_read_b128
+// pass fall in distinct bank groups. The activation fragment and its scale still come
+// straight into registers (they are L2-resident after the first touch).
+constexpr int kG1LdsRows = 32;
+constexpr int kG1LdsStep = kG1LdsRows * 128;                   // bytes per K-step and wavefront
+constexpr int kG1LdsDma = kG1LdsRows / 8;                      // DMA instructions per K-step
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+__device__ __forceinline__ int lds_swz(int m, int c) { return m * 128 + ((c ^ ((m >> 1) & 7)) << 4); }
+
+// vmcnt(n) with expcnt and lgkmcnt left unconstrained (gfx9 s_waitcnt encoding).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 16, "vmcnt immediate");
+  __builtin_amdgcn_s_waitcnt(N | (7 << 4) | (15 << 8));
+}
+
+template <int NG>
+__device__ __forceinline__ void stream_accumulate_g1_lds(const GemmParams& p, int e, int r0, int rows, int slice,
+                                                         int lane, const int32_t* row_token, uint8_t* ring,
+                                                         v4f (&acc)[2][NG]) {
+  using S = StreamShape<kG1>;
+  constexpr int KS = S::kSteps;
+  constexpr int NB = S::kRing;
+  constexpr int KMAIN = KS - KS % NB;
+  // VMEM instructions of one K-step, in issue order: the weight DMAs, then per row group the
+  // activation fragment (two 16-byte loads) and its scale
+  constexpr int kOps = kG1LdsDma + 3 * NG;
+  static_assert(kOps < 16, "vmcnt immediate");
+
+  // lane's DMA source of instruction j at K-step 0: ring row 8j + lane/8 (gate rows 0-15,
+  // up rows 16-31), the logical chunk stored at physical chunk lane%8
+  uint32_t woff[kG1LdsDma];
+#pragma unroll
+  for (int j = 0; j < kG1LdsDma; ++j) {
+    const int r = 8 * j + (lane >> 3);
+    const int c = (lane & 7) ^ ((r >> 1) & 7);
+    const size_t grow = (size_t)e * 2 * kInter + (r < 16 ? slice * 16 + r : kInter + slice * 16 + r - 16);
+    woff[j] = (uint32_t)(grow * kHidden + c * 16);
+  }
+  float sw_lane[2];
+  sw_lane[0] = p.w13_scale[((size_t)e * 32 + slice / 8) * kHBlocks + (lane < KS ? lane : 0)];
+  sw_lane[1] = p.w13_scale[((size_t)e * 32 + kIBlocks + slice / 8) * kHBlocks + (lane < KS ? lane : 0)];
+
+  auto issue_w = [&](int k, int s) {
+    uint8_t* dst = ring + s * kG1LdsStep;
+#pragma unroll
+    for (int j = 0; j < kG1LdsDma; ++j)
+      __builtin_amdgcn_global_load_lds(p.w13 + woff[j] + k * 128, (lds_void_t*)(dst + j * 1024), 16, 0, 0);
+  };
+  // the first steps' weight DMAs go out before the activation addresses are known
+#pragma unroll
+  for (int s = 0; s < NB - 1; ++s) issue_w(s, s);
+
+  const uint8_t* ap[NG];
+  const float* sap[NG];
+#pragma unroll
+  for (int g = 0; g < NG; ++g) {
+    const int m = g * 16 + (lane & 15);
+    const int mm = m < rows ? m : 0;
+    const int tok = row_token[r0 + mm];
+    ap[g] = p.hidden + (size_t)tok * kHidden + (lane >> 4) * 16;
+    sap[g] = p.hidden_scale + tok;
+  }
+  struct Act {
+    v8i a[NG];
+    float sa[NG];
+  };
+  auto issue_a = [&](int k, Act& st) {
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      st.a[g] = load_frag(ap[g] + k * 128);
+      st.sa[g] = sap[g][(size_t)k * p.T];   // hidden scales [56, T]
+    }
+  };
+  Act ring_a[NB];
+#pragma unroll
+  for (int s = 0; s < NB - 1; ++s) issue_a(s, ring_a[s]);
+
+#pragma unroll
+  for (int f = 0; f < 2; ++f)
+#pragma unroll
+    for (int g = 0; g < NG; ++g) acc[f][g] = v4f{0.f, 0.f, 0.f, 0.f};
+  const v4f zero = {0.f, 0.f, 0.f, 0.f};
+  auto step = [&](int k, int u) {
+    const int kn = min(k + NB - 1, KS - 1);
+    const int sn = (u + NB - 1) % NB;
+    issue_w(kn, sn);
+    issue_a(kn, ring_a[sn]);
+    __builtin_amdgcn_sched_barrier(0);
+    // step k's loads have landed once only step kn's are in flight
+    wait_vm<kOps>();
+    __builtin_amdgcn_sched_barrier(0);
+    const uint8_t* st = ring + u * kG1LdsStep;
+    v8i wf[2];
+#pragma unroll
+    for (int f = 0; f < 2; ++f) {
+      const uint8_t* b = st + f * 16 * 128;
+      wf[f] = join(*reinterpret_cast<const v4i*>(b + lds_swz(lane & 15, lane >> 4)),
+                   *reinterpret_cast<const v4i*>(b + lds_swz(lane & 15, 4 + (lane >> 4))));
+    }
+    const Act& a = ring_a[u];
+    float sc[2];
+#pragma unroll
+    for (int f = 0; f < 2; ++f) sc[f] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sw_lane[f]), k));
+#pragma unroll
+    for (int g = 0; g < NG; ++g)
+#pragma unroll
+      for (int f = 0; f < 2; ++f) {
+        const v4f d = mfma16x16x128_fp8(wf[f], a.a[g], zero);
+        acc[f][g] += d * (a.sa[g] * sc[f]);
+      }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+#pragma nounroll
+  for (int k0 = 0; k0 < KMAIN; k0 += NB) {
+#pragma unroll
+    for (int u = 0; u < NB; ++u) step(k0 + u, u);
+  }
+#pragma unroll
+  for (int u = 0; u < KS - KMAIN; ++u) step(KMAIN + u, u);
+  // the last steps reloaded the last K-step into a slot nobody reads: let those DMAs land
+  // before the ring is refilled by the next unit
+  wait_vm<0>();
+}
+
 // SwiGLU of a GEMM1 unit's accumulators for row group g: silu(X2) * X1 (kernel.py:126-129).
 __device__ __forceinline__ v4f swiglu4(const v4f& x1, const v4f& x2) {
   v4f c;
@@ -265,12 +399,15 @@ __device__ __forceinline__ v4f swiglu4(const v4f& x1, const v4f& x2) {
 
 // One work unit with its epilogue: GEMM1 writes fp32 SwiGLU rows for requant_kernel; GEMM2
 // writes or parks the weighted rows.
+// GEMM1 on row-major weights streams them through the wavefront's LDS ring `ring`
+// (kNB * kG1LdsStep bytes); the other instances do not use it.
 template <int KIND, int NG, bool PACKED = false>
 __device__ __forceinline__ void stream_unit(const GemmParams& p, int e, int r0, int rows, int slice, int lane,
-                                            const int32_t* row_token) {
+                                            const int32_t* row_token, uint8_t* ring) {
   constexpr int NF = StreamShape<KIND>::kFrags;
   v4f acc[NF][NG];
-  stream_accumulate<KIND, NG, PACKED>(p, e, r0, rows, slice, lane, row_token, acc);
+  if constexpr (KIND == kG1 && !PACKED) stream_accumulate_g1_lds<NG>(p, e, r0, rows, slice, lane, row_token, ring, acc);
+  else stream_accumulate<KIND, NG, PACKED>(p, e, r0, rows, slice, lane, row_token, acc);
   // lane: column (lane & 15) of each row group, fragment rows 4*(lane>>4) + i
 #pragma unroll
   for (int g = 0; g < NG; ++g) {
@@ -307,7 +444,7 @@ __device__ __forceinline__ void stream_unit(const GemmParams& p, int e, int r0, 
 // workspace, or in LDS for the fused dispatch below).
 template <int KIND, int MAXNG, bool PACKED = false>
 __device__ __forceinline__ void stream_units(const GemmParams& p, int n_items, const int4* items,
-                                             const int32_t* row_token) {
+                                             const int32_t* row_token, uint8_t* ring) {
   constexpr int SL = StreamShape<KIND>::kSlices;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -321,8 +458,8 @@ __device__ __forceinline__ void stream_units(const GemmParams& p, int n_items, c
     const int e = __builtin_amdgcn_readfirstlane(it.x);
     const int r0 = __builtin_amdgcn_readfirstlane(it.y);
     const int rows = __builtin_amdgcn_readfirstlane(it.z);
-    if (MAXNG == 1 || rows <= 16) stream_unit<KIND, 1, PACKED>(p, e, r0, rows, slice, lane, row_token);
-    else stream_unit<KIND, MAXNG, PACKED>(p, e, r0, rows, slice, lane, row_token);
+    if (MAXNG == 1 || rows <= 16) stream_unit<KIND, 1, PACKED>(p, e, r0, rows, slice, lane, row_token, ring);
+    else stream_unit<KIND, MAXNG, PACKED>(p, e, r0, rows, slice, lane, row_token, ring);
   }
 }
 
@@ -330,7 +467,14 @@ __device__ __forceinline__ void stream_units(const GemmParams& p, int n_items, c
 template <int KIND, int MAXNG, bool PACKED = false>
 __global__ __launch_bounds__(kStreamWaves * 64) void gemm_stream_kernel(GemmParams p) {
   const int n_items = min(p.counters[kCtrItems], p.max_items);
-  stream_units<KIND, MAXNG, PACKED>(p, n_items, reinterpret_cast<const int4*>(p.work_items), p.sorted_token);
+  if constexpr (KIND == kG1 && !PACKED) {
+    __shared__ __attribute__((aligned(1024))) uint8_t ring[kStreamWaves][StreamShape<kG1>::kRing * kG1LdsStep];
+    stream_units<KIND, MAXNG, PACKED>(p, n_items, reinterpret_cast<const int4*>(p.work_items), p.sorted_token,
+                                      ring[threadIdx.x >> 6]);
+  } else {
+    stream_units<KIND, MAXNG, PACKED>(p, n_items, reinterpret_cast<const int4*>(p.work_items), p.sorted_token,
+                                      nullptr);
+  }
 }
 
 // Decode batches of up to kFusedDispatchTokens tokens: GEMM1 without a dispatch launch before
@@ -346,7 +490,11 @@ constexpr int kFusedItems = kExpertsLocal + kFusedSlots / kFusedItemRows;
 constexpr int kFusedHalves = kFusedSlots / (kStreamWaves * 64);
 static_assert(kFusedHalves == 2, "two slots per thread");
 
+// The row-major instance's LDS weight rings live in the same object as the dispatch (one
+// __shared__ object: the compiler then keeps the ring's DMA writes apart from its reads).
+template <bool RING>
 struct FusedDispatch {
+  uint8_t ring[RING ? kStreamWaves : 0][StreamShape<kG1>::kRing * kG1LdsStep];
   int4 items[kFusedItems];
   int32_t row_token[kFusedSlots];
   int cnt[kFusedHalves * kStreamWaves][kExpertsLocal];   // per-wavefront counts -> prefix
@@ -354,7 +502,8 @@ struct FusedDispatch {
   int n_items;
 };
 
-__device__ __forceinline__ void fused_dispatch(const GemmParams& p, const RouteParams& rp, FusedDispatch& s) {
+template <bool RING>
+__device__ __forceinline__ void fused_dispatch(const GemmParams& p, const RouteParams& rp, FusedDispatch<RING>& s) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -453,9 +602,11 @@ __device__ __forceinline__ void fused_dispatch(const GemmParams& p, const RouteP
 // PACKED: p.w13 is the packed copy of W13 (moe_fp8_run_packed).
 template <bool PACKED>
 __global__ __launch_bounds__(kStreamWaves * 64) void gemm1_stream_dispatch_kernel(GemmParams p, RouteParams rp) {
-  __shared__ FusedDispatch s;
+  __shared__ __attribute__((aligned(1024))) FusedDispatch<!PACKED> s;
   fused_dispatch(p, rp, s);
-  stream_units<kG1, 1, PACKED>(p, s.n_items, s.items, s.row_token);
+  uint8_t* ring = nullptr;
+  if constexpr (!PACKED) ring = s.ring[threadIdx.x >> 6];
+  stream_units<kG1, 1, PACKED>(p, s.n_items, s.items, s.row_token, ring);
 }
 
 // Requantises the fp32 SwiGLU rows: per row and COLS columns, scale = max(amax/448, 1e-12)
@@ -528,10 +679,25 @@ struct SliceStage {
   float wt;         // routing weight of the lane's row
 };
 
+// On the row-major weights the slice's 28 W2 rows of a K-step (rows past 28 repeating the
+// last) go through a wavefront-private LDS ring, 8 whole rows per global_load_lds
+// instruction, as for GEMM1's row-major units; the ring and the token accumulators are one
+// LDS object.
+constexpr int kSliceLdsRows = 16 * kSliceF;                     // 32
+constexpr int kSliceLdsStep = kSliceLdsRows * 128;              // 4 KB per K-step
+constexpr int kSliceLdsDma = kSliceLdsRows / 8;                 // 4 DMA instructions
+
+template <bool RING>
+struct SliceShared {
+  float acc[kSliceQuarters][kFusedDispatchTokens][16 * kSliceF];
+  uint8_t ring[RING ? kSliceQuarters : 0][kSliceRing * kSliceLdsStep];
+};
+
 // PACKED: p.w2 is the packed copy of W2 (moe_fp8_run_packed).
 template <bool PACKED>
 __global__ __launch_bounds__(kSliceQuarters * 64) void gemm2_slice_kernel(GemmParams p) {
-  __shared__ __attribute__((aligned(16))) float acc_lds[kSliceQuarters][kFusedDispatchTokens][16 * kSliceF];
+  __shared__ __attribute__((aligned(1024))) SliceShared<!PACKED> sh;
+  auto& acc_lds = sh.acc;
   const int lane = threadIdx.x & 63;
   const int q = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int m = lane & 15;
@@ -555,15 +721,26 @@ __global__ __launch_bounds__(kSliceQuarters * 64) void gemm2_slice_kernel(GemmPa
         const int r0 = __builtin_amdgcn_readlane(my_item.y, it);
         const int rows = __builtin_amdgcn_readlane(my_item.z, it);
         const int r = r0 + (m < rows ? m : 0);
+        if constexpr (!PACKED) {
+          // the DMAs first: the wait before the fragments are read counts the later loads
+          uint8_t* dst = sh.ring[q] + (st % kSliceRing) * kSliceLdsStep;
+#pragma unroll
+          for (int j = 0; j < kSliceLdsDma; ++j) {
+            const int rr = 8 * j + (lane >> 3);
+            const int c = (lane & 7) ^ ((rr >> 1) & 7);
+            const int hr = h0 + min(rr, kSliceRows - 1);
+            __builtin_amdgcn_global_load_lds(p.w2 + ((size_t)e * kHidden + hr) * kInter + ks * 128 + c * 16,
+                                             (lds_void_t*)(dst + j * 1024), 16, 0, 0);
+          }
+        }
 #pragma unroll
         for (int f = 0; f < kSliceF; ++f) {
           // the lane's hidden row in fragment f (rows past the slice repeat its last row)
-          const int hr = h0 + 16 * f + min(m, kSliceRows - 16 * f - 1);
-          if constexpr (PACKED)
+          if constexpr (PACKED) {
+            const int hr = h0 + 16 * f + min(m, kSliceRows - 16 * f - 1);
             g.w[f] = load_frag_packed(p.w2 + (((size_t)e * (kHidden / 16) + (hr >> 4)) * kIBlocks + ks) * kPackedFrag +
                                       ((hr & 15) + 16 * (lane >> 4)) * 32);
-          else
-            g.w[f] = load_frag(p.w2 + ((size_t)e * kHidden + hr) * kInter + ks * 128 + (lane >> 4) * 16);
+          }
           const int orow = h0 + min(16 * f + 4 * (lane >> 4), kSliceRows - 1);   // first output row
           g.sw[f] = p.w2_scale[((size_t)e * kHBlocks + orow / kBlock) * kIBlocks + ks];
         }
@@ -585,6 +762,26 @@ __global__ __launch_bounds__(kSliceQuarters * 64) void gemm2_slice_kernel(GemmPa
           issue(st0 + u + kSliceRing - 1, ring[(u + kSliceRing - 1) % kSliceRing]);
           __builtin_amdgcn_sched_barrier(0);
           const SliceStage& g = ring[u % kSliceRing];
+          v8i wf[kSliceF];
+          if constexpr (PACKED) {
+#pragma unroll
+            for (int f = 0; f < kSliceF; ++f) wf[f] = g.w[f];
+          } else {
+            // step st0 + u has landed once only the loads of the step just issued are in
+            // flight: 4 DMAs, 2 weight scales, the act fragment (2) and its scales, plus the
+            // rows' tokens and weights when that step is an item's last (the only step whose
+            // are read). Covering every load of step st0 + u here also keeps the compiler
+            // from waiting on the rest itself, which it would do with vmcnt(0) while the
+            // ring's DMAs are in flight.
+            if (u == kSliceSteps - 2) wait_vm<kSliceLdsDma + 7>();
+            else wait_vm<kSliceLdsDma + 5>();
+            __builtin_amdgcn_sched_barrier(0);
+            const uint8_t* b = sh.ring[q] + (u % kSliceRing) * kSliceLdsStep;
+#pragma unroll
+            for (int f = 0; f < kSliceF; ++f)
+              wf[f] = join(*reinterpret_cast<const v4i*>(b + f * 2048 + lds_swz(m, lane >> 4)),
+                           *reinterpret_cast<const v4i*>(b + f * 2048 + lds_swz(m, 4 + (lane >> 4))));
+          }
           // the act fragment's two 64-column halves carry their own scales: one MFMA per
           // half, the other half's bytes zeroed (lanes hold bytes [16j, 16j+16) of the first
           // half in a[0..3] and of the second in a[4..7])
@@ -594,8 +791,8 @@ __global__ __launch_bounds__(kSliceQuarters * 64) void gemm2_slice_kernel(GemmPa
 #pragma unroll
           for (int f = 0; f < kSliceF; ++f) {
             const float sc_lo = g.sa.x * g.sw[f], sc_hi = g.sa.y * g.sw[f];
-            const v4f d_lo = mfma16x16x128_fp8(g.w[f], a_lo, zero);
-            const v4f d_hi = mfma16x16x128_fp8(g.w[f], a_hi, zero);
+            const v4f d_lo = mfma16x16x128_fp8(wf[f], a_lo, zero);
+            const v4f d_hi = mfma16x16x128_fp8(wf[f], a_hi, zero);
             acc[f] += d_lo * sc_lo;
             acc[f] += d_hi * sc_hi;
           }
@@ -607,7 +804,9 @@ __global__ __launch_bounds__(kSliceQuarters * 64) void gemm2_slice_kernel(GemmPa
         const SliceStage& g = ring[(kSliceSteps - 1) % kSliceRing];
         const int rows = __builtin_amdgcn_readlane(my_item.z, st0 / kSliceSteps);
         const bool live = m < rows;
-        const int prev = __shfl(g.tok, lane - 1);
+        // token of the row above (DPP row shift: a data-share permute here would make the
+        // compiler drain the ring's loads in flight)
+        const int prev = __builtin_amdgcn_update_dpp(g.tok, g.tok, 0x111, 0xf, 0xf, false);
         const bool head = live && (m == 0 || prev != g.tok);
         const bool dups = __ballot(live && !head) != 0;
 #pragma unroll
@@ -630,6 +829,8 @@ __global__ __launch_bounds__(kSliceQuarters * 64) void gemm2_slice_kernel(GemmPa
           if (head) *reinterpret_cast<v4f*>(&acc_lds[q][g.tok][16 * f + 4 * (lane >> 4)]) += v;
         }
       }
+      // the last steps reloaded the last K-step into a ring slot nobody reads
+      if constexpr (!PACKED) wait_vm<0>();
     }
     __syncthreads();
     // the four K quarters, summed in fixed order: 4 columns of one token per thread (the slice's
