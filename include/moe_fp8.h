@@ -113,14 +113,14 @@ typedef struct moe_fp8_args {
  *   counters      int32 [80]        [0] number of work items, [1] N; the rest internal
  *                                   (the tile kernels' work-list state)
  *   act           fp8   [N_max, 2048]    SwiGLU output requantised to e4m3fn          (kernel.py:669)
- *   act_scale     fp32  [N_max, 2048/requant_block]  its 1 x requant_block scales, row-major
- *                                        per row                                      (kernel.py:670)
- *                 requant_block is 64 up to 64 tokens, the reference's 1x64 block (BLOCK_N_1 = 64,
- *                 kernel.py:131-135, :643, scales [32, N]). Above 64 tokens it is 128, a
+ *   act_scale     fp32  [N_max, 32]    its 1 x requant_block scales, row-major per row,
+ *                                        2048/requant_block of them              (kernel.py:670)
+ *                 requant_block is 64 below 4096 tokens, the reference's 1x64 block (BLOCK_N_1 =
+ *                 64, kernel.py:131-135, :643, scales [32, N]). From 4096 tokens on it is 128, a
  *                 deliberate difference: GEMM2 then applies one activation scale per 128-wide K
- *                 block, like every other operand. The parity tests bound the output's distance
- *                 from fp32 math by that of the 64-column algorithm (per token at most 2x its
- *                 maximum error + 1/64).
+ *                 block, like every other operand, with one MFMA per fragment instead of two.
+ *                 The parity tests bound the output's distance from fp32 math by that of the
+ *                 64-column algorithm (per token at most 2x its maximum error + 1/64).
  *   partial       fp32  [T*8, 7168]      weighted GEMM2 rows of tokens with more than one local
  *                                        assignment, indexed by flat slot, above 64 tokens (0
  *                                        bytes up to 64: the combine happens inside GEMM2)
@@ -151,7 +151,7 @@ typedef struct moe_fp8_layout {
   int32_t max_work_items;
   int32_t route_blocks;      /* routing work-groups */
   int32_t rows_per_item;     /* GEMM rows (assignments) per work item */
-  int32_t requant_block;     /* columns per act_scale entry: 64 up to 64 tokens, else 128 */
+  int32_t requant_block;     /* columns per act_scale entry: 64 below 4096 tokens, else 128 */
   int32_t reserved[2];
 } moe_fp8_layout;
 
@@ -240,7 +240,7 @@ int moe_fp8_route_dispatch(const moe_fp8_args* args, int32_t skip_routing, void*
 
 /* Stage 2: GEMM1 over the gathered tokens of each local expert and SwiGLU (silu of the
  * second half times the first half). One kernel. Reads the dispatch arrays; writes the
- * fp8 intermediate act/act_scale (one scale per row per 128 columns) when
+ * fp8 intermediate act/act_scale (one scale per row per requant_block columns) when
  * layout.rows_per_item > 32, otherwise the fp32 SwiGLU rows `swiglu`, which stage 3
  * requantises first.
  * Replaces the token pack and moe_gemm1_kernel (kernel.py:663-693, 7-151). */

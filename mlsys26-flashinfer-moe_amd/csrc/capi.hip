@@ -146,12 +146,14 @@ int compute_layout(int32_t T, moe_fp8_layout* out) {
   L.slot_rank = take(t * kTopK * sizeof(int32_t));
   L.block_count = take((size_t)blocks * kExpertsLocal * sizeof(int32_t));
   L.work_items = take((size_t)max_items * 4 * sizeof(int32_t));
-  // Items of up to 32 rows keep GEMM1's fp32 SwiGLU rows for requant_kernel (per 64 columns
-  // with 16-row items, per 128 with 32-row items); the tile GEMM1 requantises per 128 columns
-  // in its epilogue. With 16-row items (up to 64 tokens) GEMM2 combines in LDS: no parked rows.
+  // Items of up to 32 rows keep GEMM1's fp32 SwiGLU rows for requant_kernel; the tile GEMM1
+  // requantises in its epilogue. Up to 128-row items the blocks are 64 columns wide, 128 with
+  // 160-row items; the scale array is sized for 64 either way, so that the workspace size
+  // stays non-decreasing in T. With 16-row items (up to 64 tokens) GEMM2 combines in LDS: no
+  // parked rows.
   const int rb = requant_block_for(rpi);
   L.act = take(nmax * kInter);
-  L.act_scale = take(nmax * (kInter / rb) * sizeof(float));
+  L.act_scale = take(nmax * (kInter / 64) * sizeof(float));
   L.partial = take(rpi == 16 ? 0 : t * kTopK * kHidden * sizeof(float));
   L.swiglu = take(rpi <= 32 ? nmax * kInter * sizeof(float) : 0);
   L.total_bytes = off;

@@ -69,10 +69,17 @@ constexpr int kWDma = kTileW / kTileWaves / 8;       // weight DMA loads per wav
 // Shape of the kernel for items of up to ROWS rows (kTileItemRowsMid or kTileItemRowsLarge).
 // Per K-step every wavefront issues kLoadsPerStep loads: its 32 weight rows (kWDma loads),
 // the activation row blocks w and w+8 of the tile (8 rows each) and a third load:
-//   128 rows: the scales of one 64-row block (block w%4 capped at the last one; a load that
+//   128 rows: the scales of one 64-row block: GEMM1 block w%4, GEMM2 block (w/2)%4 and
+//             64-column half w%2 of the K-step (both capped at the last block; a load that
 //             repeats another writes the same bytes to the same LDS slots);
 //   160 rows: activation block w+16 for waves 0-3, and the scales of 64-row block w-4
 //             (capped at the last one) for waves 4-7.
+// Columns per requantisation scale of GEMM1's output (kQCols): the reference's 64
+// (kernel.py:131-135) with 128-row items, so that GEMM2 applies two activation scales per
+// 128-wide K-step (one MFMA per 64-column half, the other half's bytes zeroed); 128 with
+// 160-row items (T >= 4096), one scale and one MFMA per fragment. Measured with 64 there
+// too: GEMM2 + combine 249 -> 323 us at T=8192 and 552 -> 732 us on the skewed T=4096 batch
+// (its MFMAs double), against 115 -> 121 us at T=1024.
 template <int ROWS>
 struct TileShape {
   static constexpr int kRows = ROWS;
@@ -80,10 +87,14 @@ struct TileShape {
   static constexpr bool kThirdBlock = kABlocks > 2 * kTileWaves;   // waves 0-3 load block w+16
   static constexpr int kSBlocks = (ROWS + 63) / 64;       // 64-row scale blocks
   static constexpr int kSSlots = 64 * kSBlocks;
+  static constexpr int kQCols = ROWS == kTileItemRowsMid ? 64 : 128;
+  static constexpr int kQBlocks = kInter / kQCols;        // activation scales per row
+  static constexpr int kSHalves = kBlock / kQCols;        // GEMM2 activation scales per K-step
   static constexpr int kMaxNG = (ROWS / 16 + 1) / 2;      // row groups of a wavefront half
   static constexpr int kLoadsPerStep = kWDma + 3;
   static_assert(ROWS % 16 == 0 && (kABlocks == 2 * kTileWaves || kABlocks == 2 * kTileWaves + 4), "tile rows");
   static_assert(kSBlocks <= 4, "scale blocks");
+  static_assert(kSHalves == 1 || !kThirdBlock, "two scale halves only with the 128-row load plan");
 };
 
 typedef __attribute__((address_space(3))) void lds_void;
@@ -108,7 +119,8 @@ template <int ROWS>
 struct TileStage {
   uint8_t w[kTileW * 128];
   uint8_t a[ROWS * 128];
-  float sa[TileShape<ROWS>::kSSlots];   // scale of item row m at m
+  // scale of item row m at m (GEMM2 with two per K-step: the second half's at kSSlots + m)
+  float sa[TileShape<ROWS>::kSHalves * TileShape<ROWS>::kSSlots];
 };
 
 // The ring and the next list entry share one LDS object: with a second __shared__
@@ -119,7 +131,8 @@ struct TileShared {
   TileStage<ROWS> st[kStages];
   int next;
 };
-static_assert(sizeof(TileShared<kTileItemRowsLarge>) <= 160 * 1024, "LDS of one CU");
+static_assert(sizeof(TileShared<kTileItemRowsLarge>) <= 160 * 1024 && sizeof(TileShared<kTileItemRowsMid>) <= 160 * 1024,
+              "LDS of one CU");
 static_assert(4 * kTileItemRowsLarge * sizeof(float) <= kTileW * 128, "amax fits in a weight tile");
 
 // Per-work-unit pointers of one lane.
@@ -129,6 +142,7 @@ struct TileCtx {
   uint32_t woff[kWDma];        // weight DMA byte offsets (row + permuted 16-byte chunk); < 2^30
   const uint8_t* asrc[3];      // activation DMA sources of blocks w, w+8 (and w+16)
   int sblk;                    // the 64-row scale block this wave loads
+  int shalf;                   // GEMM2 with 64-column scales: the half of the K-step it loads
   const float* ssrc;           // activation scale DMA source (waves 4-7)
   size_t sstride;              // scale stride between K blocks
   float sw0_lane, sw1_lane;     // lane k: weight block scale of K-step k of fragments 0,1
@@ -155,6 +169,8 @@ __device__ __forceinline__ void tile_body(const GemmParams& p, const TileCtx<ROW
                                           int32_t* queue) {
   using S = TileShape<ROWS>;
   constexpr int KS = G1 ? kHBlocks : kIBlocks;
+  // GEMM2 with two activation scales per K-step (64-column requantisation blocks)
+  constexpr bool H2 = !G1 && S::kSHalves == 2;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wb = wave & 3;     // weight rows 64*wb.. (item rows: the wave's half, from c.m0)
@@ -184,7 +200,7 @@ __device__ __forceinline__ void tile_body(const GemmParams& p, const TileCtx<ROW
       if (wave < 4) dma16((nxt ? n.asrc[2] : c.asrc[2]) + k * 128, &st.a[8 * (wave + 2 * kTileWaves) * 128]);
       else dma4(sk, &st.sa[64 * c.sblk]);
     } else {
-      dma4(sk, &st.sa[64 * c.sblk]);
+      dma4(sk, &st.sa[S::kSSlots * c.shalf + 64 * c.sblk]);
     }
   };
 
@@ -209,12 +225,14 @@ __device__ __forceinline__ void tile_body(const GemmParams& p, const TileCtx<ROW
     v8i wf[4];
     v8i bf;
     float sa;
+    float sa2;   // H2: the scale of the K-step's second 64-column half
   };
   auto load_head = [&](int s, Head& h) {
     if constexpr (NG > 0) {
       const TileStage<ROWS>& st = sh.st[s];
       h.bf = lds_frag(st.a + c.m0 * 128, lane & 15, lane);
       h.sa = st.sa[c.m0 + (lane & 15)];
+      h.sa2 = H2 ? st.sa[S::kSSlots + c.m0 + (lane & 15)] : 0.f;
 #pragma unroll
       for (int f = 0; f < 4; ++f) h.wf[f] = lds_frag(st.w, wrow(f), lane);
     }
@@ -225,7 +243,8 @@ __device__ __forceinline__ void tile_body(const GemmParams& p, const TileCtx<ROW
   // the first group of the next step runs), so that the matrix core is not idle during the
   // VALU work. dp holds the pending group's MFMA results, p0/p1 its two scale products.
   v4f dp[4] = {zero, zero, zero, zero};
-  float p0 = 0.f, p1 = 0.f;
+  v4f dp2[4] = {zero, zero, zero, zero};   // H2: the second half's pending results
+  float p0 = 0.f, p1 = 0.f, p2 = 0.f;
 
   auto compute = [&](int s, const Head& h, float s0, float s1) __attribute__((always_inline)) {
     if constexpr (NG > 0) {
@@ -233,33 +252,55 @@ __device__ __forceinline__ void tile_body(const GemmParams& p, const TileCtx<ROW
       const v8i (&wf)[4] = h.wf;
       v8i bf = h.bf;
       float sa = h.sa;
+      float sa2 = h.sa2;
 #pragma unroll
       for (int g = 0; g < NG; ++g) {
         // the next row group's fragment is read from LDS while this group's MFMAs run
         v8i bf_next = bf;
         float sa_next = sa;
+        float sa2_next = sa2;
         if (g + 1 < NG) {
           bf_next = lds_frag(st.a + c.m0 * 128, 16 * (g + 1) + (lane & 15), lane);
           sa_next = st.sa[c.m0 + 16 * (g + 1) + (lane & 15)];
+          if constexpr (H2) sa2_next = st.sa[S::kSSlots + c.m0 + 16 * (g + 1) + (lane & 15)];
         }
         // pending group: the previous group of this step, or the previous step's last
         // group (zero results and zero scales before the first step)
         const int gp = g == 0 ? NG - 1 : g - 1;
-        v4f d[4];
+        v4f d[4], d2[4];
+        if constexpr (H2) {
+          // one MFMA per 64-column half of the activation fragment (lanes hold bytes
+          // [16j, 16j+16) of the first half in bf[0..3] and of the second in bf[4..7])
+          const v4i kZero4 = {0, 0, 0, 0};
+          const v8i b_lo = join(lo_half(bf), kZero4);
+          const v8i b_hi = join(kZero4, hi_half(bf));
 #pragma unroll
-        for (int f = 0; f < 4; ++f) {
-          d[f] = mfma16x16x128_fp8(wf[f], bf, zero);
-          acc[f][gp] += dp[f] * (f < 2 ? p0 : p1);
+          for (int f = 0; f < 4; ++f) {
+            d[f] = mfma16x16x128_fp8(wf[f], b_lo, zero);
+            d2[f] = mfma16x16x128_fp8(wf[f], b_hi, zero);
+            acc[f][gp] += dp[f] * p0;
+            acc[f][gp] += dp2[f] * p2;
+          }
+#pragma unroll
+          for (int f = 0; f < 4; ++f) dp2[f] = d2[f];
+        } else {
+#pragma unroll
+          for (int f = 0; f < 4; ++f) {
+            d[f] = mfma16x16x128_fp8(wf[f], bf, zero);
+            acc[f][gp] += dp[f] * (f < 2 ? p0 : p1);
+          }
         }
 #pragma unroll
         for (int f = 0; f < 4; ++f) dp[f] = d[f];
         p0 = sa * s0;
         p1 = sa * s1;
+        if constexpr (H2) p2 = sa2 * s0;
         // two row groups' MFMA results live at a time (the scheduler would otherwise hoist
         // every MFMA of the step and hold all their results)
         __builtin_amdgcn_sched_barrier(0);
         bf = bf_next;
         sa = sa_next;
+        sa2 = sa2_next;
       }
     }
   };
@@ -296,7 +337,10 @@ __device__ __forceinline__ void tile_body(const GemmParams& p, const TileCtx<ROW
   // the last step's last row group
   if constexpr (NG > 0) {
 #pragma unroll
-    for (int f = 0; f < 4; ++f) acc[f][NG - 1] += dp[f] * (f < 2 ? p0 : p1);
+    for (int f = 0; f < 4; ++f) {
+      acc[f][NG - 1] += dp[f] * (f < 2 ? p0 : p1);
+      if constexpr (H2) acc[f][NG - 1] += dp2[f] * p2;
+    }
   }
   // The loads in flight now are the next unit's first two steps, or reloads nobody reads; the
   // reloads must land before the next unit refills the ring.
@@ -307,11 +351,12 @@ __device__ __forceinline__ void tile_body(const GemmParams& p, const TileCtx<ROW
   if (queue != nullptr && threadIdx.x == 0) got = atomicAdd(queue, 1);
 
   if constexpr (G1) {
-    // SwiGLU (kernel.py:126-129) and 1x128 requantisation (kernel.py:131-135 with 128
-    // columns): the tile's 128 columns are one scale block, spread over the 4 wavefronts
-    // that share this wave's item rows. Their row amax meet in the weight tile of the stage
-    // of the unit's last step, which no load targets until the next unit's first step; the
-    // barrier shows that every wave is done reading it.
+    // SwiGLU (kernel.py:126-129) and requantisation per S::kQCols columns (kernel.py:131-135):
+    // the tile's 128 columns are spread over the 4 wavefronts that share this wave's item
+    // rows, 32 each, so a 64-column block is two of them and a 128-column block all four.
+    // Their row amax meet in the weight tile of the stage of the unit's last step, which no
+    // load targets until the next unit's first step; the barrier shows that every wave is
+    // done reading it.
     float(*amax_buf)[ROWS] = reinterpret_cast<float(*)[ROWS]>(sh.st[(s_base + KS - 1) % kStages].w);
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __builtin_amdgcn_s_barrier();
@@ -336,7 +381,9 @@ __device__ __forceinline__ void tile_body(const GemmParams& p, const TileCtx<ROW
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
       const int m = c.m0 + 16 * g + (lane & 15);
-      const float amax = fmaxf(fmaxf(amax_buf[0][m], amax_buf[1][m]), fmaxf(amax_buf[2][m], amax_buf[3][m]));
+      const float amax = S::kQCols == 64
+                             ? fmaxf(amax_buf[wb & 2][m], amax_buf[(wb & 2) + 1][m])
+                             : fmaxf(fmaxf(amax_buf[0][m], amax_buf[1][m]), fmaxf(amax_buf[2][m], amax_buf[3][m]));
       const float scale = fmaxf(amax / 448.0f, 1e-12f);
       if (m < c.rows) {
         uint8_t* dst = p.act + (size_t)(c.r0 + m) * kInter + c.tile * 128 + 32 * wb + 4 * (lane >> 4);
@@ -344,7 +391,9 @@ __device__ __forceinline__ void tile_body(const GemmParams& p, const TileCtx<ROW
         for (int h = 0; h < 2; ++h)
           *reinterpret_cast<uint32_t*>(dst + 16 * h) =
               pack_fp8x4(cval[g][h][0] / scale, cval[g][h][1] / scale, cval[g][h][2] / scale, cval[g][h][3] / scale);
-        if (wb == 0 && lane < 16) p.act_scale[(size_t)(c.r0 + m) * kIBlocks + c.tile] = scale;
+        // the first wave of each scale block writes the block's scale
+        if ((wb & (S::kQCols / 32 - 1)) == 0 && lane < 16)
+          p.act_scale[(size_t)(c.r0 + m) * S::kQBlocks + (c.tile * 128 + 32 * wb) / S::kQCols] = scale;
       }
     }
     __syncthreads();
@@ -438,14 +487,16 @@ __device__ __forceinline__ void unit_setup(const GemmParams& p, int u, TileCtx<R
     c.asrc[j] = (G1 ? p.hidden : p.act) + row + ch * 16;
   }
   {
-    // the wave's 64-row block of scales: w % 4 (128 rows) or w - 4 (160 rows, waves 4-7),
-    // capped at the last block
-    c.sblk = min(S::kThirdBlock ? max(wave - 4, 0) : (wave & 3), S::kSBlocks - 1);
+    // the wave's 64-row block of scales: w % 4 (128 rows; GEMM2 with two scales per K-step
+    // (w / 2) % 4, half w % 2) or w - 4 (160 rows, waves 4-7), capped at the last block
+    constexpr bool H2 = !G1 && S::kSHalves == 2;
+    c.sblk = min(S::kThirdBlock ? max(wave - 4, 0) : (H2 ? (wave >> 1) & 3 : (wave & 3)), S::kSBlocks - 1);
+    c.shalf = H2 ? (wave & 1) : 0;
     const int m = 64 * c.sblk + lane;
     const int mm = m < c.rows ? m : 0;
     if constexpr (G1) c.ssrc = p.hidden_scale + p.sorted_token[c.r0 + mm];
-    else c.ssrc = p.act_scale + (size_t)(c.r0 + mm) * kIBlocks;
-    c.sstride = G1 ? (size_t)p.T : 1;
+    else c.ssrc = p.act_scale + (size_t)(c.r0 + mm) * S::kQBlocks + c.shalf;
+    c.sstride = G1 ? (size_t)p.T : (size_t)S::kSHalves;
   }
   const float* swp0;
   const float* swp1;

@@ -77,9 +77,10 @@ inline int rows_per_item_for(int T) {
 }
 
 // Columns per requantisation scale of the GEMM1 output: the reference's 64 (kernel.py:131-135)
-// on the streaming path (items of up to 32 rows, up to 256 tokens), 128 on the tile path (one
-// activation scale per 128-wide K block of the tile GEMM2).
-inline int requant_block_for(int rows_per_item) { return rows_per_item <= 32 ? 64 : 128; }
+// with items of up to 128 rows (below 4096 tokens), 128 with the 160-row items of larger
+// batches (one activation scale, and one MFMA per fragment, per 128-wide K block of the tile
+// GEMM2).
+inline int requant_block_for(int rows_per_item) { return rows_per_item <= kTileItemRowsMid ? 64 : 128; }
 
 int compute_layout(int32_t T, moe_fp8_layout* out);
 
@@ -126,7 +127,7 @@ struct GemmParams {
   const int32_t* sorted_slot;
   const int32_t* token_nlocal;
   uint8_t* act;                // [N_max, 2048]
-  float* act_scale;            // [N_max, 16]
+  float* act_scale;            // [N_max, 2048 / requantisation block]
   float* partial;              // [T*8, 7168]
   float* swiglu;               // [N_max, 2048] (decode path)
   void* out;                   // [T, 7168]

@@ -9,8 +9,8 @@ mode="definition": the intermediate C stays fp32 (the definition's math); each t
   output sums its experts' weighted rows in ascending expert order, as the definition's
   loop over experts does.
 mode="emulated":   C is requantised to e4m3 with one scale per row per `requant_block`
-  columns before GEMM2 (kernel.py:131-135 uses 64; the HIP kernels use 64 up to 64 tokens
-  and 128 above), and each token sums its weighted rows in top-k slot order starting from
+  columns before GEMM2 (kernel.py:131-135 uses 64; the HIP kernels use 64 below 4096 tokens
+  and 128 from 4096 on), and each token sums its weighted rows in top-k slot order starting from
   0, as the HIP combine does; a token with one local assignment gets exactly that row.
   With `act_override` = (act uint8 [N, I], act_scale fp32 [N, I/requant_block]) in
   bucket-row order, GEMM1 is skipped and GEMM2 + combine run on that intermediate instead

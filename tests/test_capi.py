@@ -51,17 +51,17 @@ def test_layout_consistent(pkg, T):
     assert L.max_work_items == 32 + (8 * T + L.rows_per_item - 1) // L.rows_per_item
     assert L.counters == 0
     # up to 64 tokens (16-row items) GEMM2 combines in LDS (no parked rows); items of up to 32
-    # rows (up to 256 tokens) keep GEMM1's fp32 SwiGLU rows and requantise per 64 columns, the
-    # reference's block; the tile path per 128
+    # rows (up to 256 tokens) keep GEMM1's fp32 SwiGLU rows; up to 128-row items (below 4096
+    # tokens) requantise per 64 columns, the reference's block; the 160-row items per 128
     decode = L.rows_per_item == 16
     assert L.rows_per_item == (16 if T <= 64 else 32 if T <= 256 else L.rows_per_item)
-    assert L.requant_block == (64 if L.rows_per_item <= 32 else 128)
+    assert L.requant_block == (64 if L.rows_per_item <= 128 else 128)
     arrays = [
         ("topk_ids", 4 * 8 * T), ("topk_weights", 4 * 8 * T), ("expert_count", 4 * 32),
         ("expert_start", 4 * 33), ("sorted_token", 4 * 8 * T), ("sorted_weight", 4 * 8 * T),
         ("sorted_slot", 4 * 8 * T), ("token_nlocal", 4 * T), ("slot_rank", 4 * 8 * T),
         ("block_count", 4 * 32 * L.route_blocks), ("work_items", 16 * L.max_work_items),
-        ("counters", 4 * 80), ("act", 8 * T * 2048), ("act_scale", 4 * 8 * T * 2048 // L.requant_block),
+        ("counters", 4 * 80), ("act", 8 * T * 2048), ("act_scale", 4 * 8 * T * 2048 // 64),
         ("partial", 0 if decode else 4 * 8 * T * 7168),
         ("swiglu", 4 * 8 * T * 2048 if L.rows_per_item <= 32 else 0),
     ]

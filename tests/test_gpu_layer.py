@@ -2,8 +2,8 @@
 
 The layer is checked in two halves and as a whole, on bf16 output compared as float32:
   * GEMM1 + SwiGLU + requantisation, through the fp8 intermediate it leaves in the
-    workspace, against the emulated oracle (the kernels' algorithm: 1x64 requantisation up
-    to 64 tokens, as the reference's, and 1x128 above; the layout reports which):
+    workspace, against the emulated oracle (the kernels' algorithm: 1x64 requantisation
+    below 4096 tokens, as the reference's, and 1x128 from 4096 on; the layout reports which):
     scales within 3e-4 relative, at most 1% of the bytes different, each by at most one
     fp8 step (plus 4e-4 of the row maximum for the MFMA's block-sum precision).
   * GEMM2 + weighted combine, on exactly that intermediate (the oracle's act_override):
@@ -16,8 +16,8 @@ The layer is checked in two halves and as a whole, on bf16 output compared as fl
     every element of the token's output row moves by a few hundredths.)
   * The whole layer against the definition (fp32 intermediate, kernel.py's math without
     requantisation): relative RMS <= 0.05; and against the reference's own algorithm, which
-    requantises per 64 columns (kernel.py:131-135) where these kernels use 128 above 64
-    tokens (below, the same algorithm in another summation order), per token
+    requantises per 64 columns (kernel.py:131-135) where these kernels use 128 from 4096
+    tokens on (below, the same algorithm in another summation order), per token
         max_j |gpu - def| <= 2 * max_j |ref64 - def| + 1/64,
     and over all checked elements rms(gpu - def) <= 1.25 * rms(ref64 - def). The factor 2:
     on the CPU the 128-column algorithm's per-token maximum reaches 1.56x the 64-column
@@ -104,7 +104,7 @@ def _run_full(kw, out_dtype=torch.bfloat16):
 def _requant_block(T):
     """Columns per activation scale of the layer at T tokens, from the library's layout."""
     rb = int(_gh()._lib.workspace_layout(T).requant_block)
-    assert rb == (64 if T <= 256 else 128)
+    assert rb == (64 if T < 4096 else 128)
     return rb
 
 
