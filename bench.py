@@ -81,19 +81,20 @@ def routing_stats(ws, T):
     return n, e_touched, u
 
 
-def workload_figures(T, n, e_touched, u, rows_per_item):
+def workload_figures(T, n, e_touched, u, rows_per_item, requant_block=128):
     """Algorithmic work of the layer and of its GEMM1 kernel. GEMM1 reads the touched experts'
     W13 and block scales and each token's hidden row and scales once. Per assignment it writes,
     in the decode regime (items of <= 32 rows), the fp32 SwiGLU row (8,192 B), and up to 64
     tokens it reads the top-k lists (64 B per token) for the dispatch it rebuilds; on the tile
-    path it writes the requantised fp8 row and its 16 scales (2,112 B)."""
+    path it writes the requantised fp8 row and its 2048 / requant_block scales (2,176 B with
+    64-column blocks, 2,112 B with 128)."""
     layer_bytes = e_touched * BYTES_PER_EXPERT + T * BYTES_PER_TOKEN + 512
     layer_flops = n * FLOPS_PER_ASSIGNMENT
     g1_bytes = e_touched * G1_BYTES_PER_EXPERT + u * (7168 + 224)
     if rows_per_item <= 32:
         g1_bytes += n * 2048 * 4 + (T * 64 if rows_per_item == 16 else 0)
     else:
-        g1_bytes += n * (2048 + 16 * 4)
+        g1_bytes += n * (2048 + (2048 // requant_block) * 4)
     return dict(layer_bytes=layer_bytes, layer_flops=layer_flops, g1_bytes=g1_bytes,
                 g1_flops=n * G1_FLOPS_PER_ASSIGNMENT, g2_flops=n * G2_FLOPS_PER_ASSIGNMENT)
 
@@ -245,7 +246,7 @@ def bench_workload(pkg, inputs, name, weight_sets, steps, warmup):
     del qsets
 
     rpi = int(ws.layout.rows_per_item)
-    f = workload_figures(T, n, e_touched, u, rpi)
+    f = workload_figures(T, n, e_touched, u, rpi, int(ws.layout.requant_block))
     us = ms_per_step * 1e3
     res = dict(T=T, offset=wl.local_expert_offset, assignments=n, experts_touched=e_touched,
                us_per_step=round(us, 2), us_median_call=round(median_ms * 1e3, 2),
@@ -256,6 +257,10 @@ def bench_workload(pkg, inputs, name, weight_sets, steps, warmup):
                stage_us=dict(route_dispatch=round(stage_ms[0] * 1e3, 2), gemm1=round(stage_ms[1] * 1e3, 2),
                              requant_gemm2_combine=round(stage_ms[2] * 1e3, 2)))
     res["rows_per_item"] = rpi
+    res["requant_block"] = int(ws.layout.requant_block)
+    res["tokens_with_local"] = u
+    res["gemm1_algorithmic_bytes"] = f["g1_bytes"]
+    res["gemm1_algorithmic_flops"] = f["g1_flops"]
     if packs is not None:
         res["weights"] = "packed copy per weight set (as run() streams up to 256 tokens)"
         res["row_major_us_per_step"] = round(row_major_ms * 1e3, 2)
