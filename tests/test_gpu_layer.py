@@ -16,10 +16,13 @@ The layer is checked in two halves and as a whole, on bf16 output compared as fl
     every element of the token's output row moves by a few hundredths.)
   * The whole layer against the definition (fp32 intermediate, kernel.py's math without
     requantisation): relative RMS <= 0.05; and against the reference's own algorithm, which
-    requantises per 64 columns (kernel.py:131-135) where these kernels use 128 from 4096
-    tokens on (below, the same algorithm in another summation order), per token
-        max_j |gpu - def| <= 2 * max_j |ref64 - def| + 1/64,
-    and over all checked elements rms(gpu - def) <= 1.25 * rms(ref64 - def). The factor 2:
+    requantises per 64 columns (kernel.py:131-135). Below 4096 tokens the kernels run that
+    algorithm in another summation order, and per token
+        max_j |gpu - def| <= 1.5 * max_j |ref64 - def| + 1/64,
+    over all checked elements rms(gpu - def) <= 1.02 * rms(ref64 - def) (measured: equal to
+    four digits, per-token ratio at most 1.2, from fp8 rounding flips of the intermediate where
+    the two fp32 sums straddle a rounding boundary). From 4096 tokens on they requantise per
+    128 columns, and the factors are 2 and 1.25. The factor 2:
     on the CPU the 128-column algorithm's per-token maximum reaches 1.56x the 64-column
     one's (median 1.09x; t16, t64 and t1024_off64, every token), and the GPU's summation
     order adds its fp8 flips on top (measured up to 1.43x at T=8192 and the skewed T=4096
@@ -108,6 +111,36 @@ def _requant_block(T):
     return rb
 
 
+def _vs_reference_algorithm(g, npkw, tokens, T, name):
+    """The layer's output rows `g` (the tokens `tokens`, or all) against the fp32 definition and
+    against the reference's own algorithm (64-column requantisation, kernel.py:131-135): per
+    token and in aggregate no further from the definition than it, within the factors stated
+    at the top of this file."""
+    rms = lambda x: float(np.sqrt(np.mean(np.square(x))))
+    ref = olayer.layer_forward(**npkw, mode="definition", tokens=tokens)["output"]
+    rel = rms(g - ref) / max(rms(ref), 1e-30)
+    print(f"{name} vs definition: rel rms {rel:.4g}", flush=True)
+    assert rel <= 0.05
+    ref64 = olayer.layer_forward(**npkw, mode="emulated", requant_block=64, tokens=tokens)["output"]
+    tok_gpu = np.max(np.abs(g - ref), axis=1)
+    tok_ref = np.max(np.abs(ref64 - ref), axis=1)
+    ratio = tok_gpu / np.maximum(tok_ref, 1e-30)
+    live = tok_ref > 0
+    print(f"{name}: per-token max|gpu - def| / max|ref64 - def|: max {np.max(ratio[live], initial=0):.3f}, "
+          f"median {np.median(ratio[live]) if live.any() else 0:.3f} over {int(live.sum())} tokens", flush=True)
+    # below 4096 tokens the layer runs the reference's algorithm itself (another summation
+    # order only): held to it tightly; with 128-column blocks (from 4096 tokens) by the looser
+    # factors
+    same_algorithm = _requant_block(T) == 64
+    f_tok, f_rms = (1.5, 1.02) if same_algorithm else (2.0, 1.25)
+    bad = tok_gpu > f_tok * tok_ref + 1.0 / 64
+    assert not bad.any(), f"{name}: {int(bad.sum())} tokens beyond {f_tok} x the reference algorithm's error"
+    e_gpu, e_ref = rms(g - ref), rms(ref64 - ref)
+    print(f"{name}: rms(gpu - definition) {e_gpu:.4g}, rms(reference algorithm - definition) {e_ref:.4g}",
+          flush=True)
+    assert e_gpu <= f_rms * e_ref
+
+
 def _read_act(ws, n):
     gh = _gh()
     nb = 2048 // int(ws.layout.requant_block)
@@ -186,26 +219,7 @@ def test_layer_matches_oracle(name, sample):
     rel = rms(g - emu["output"]) / max(rms(emu["output"]), 1e-30)
     print(f"{name} vs emulated oracle: rel rms {rel:.4g}, max err {np.max(np.abs(g - emu['output'])):.4g}", flush=True)
     assert rel <= 0.01
-    ref = olayer.layer_forward(**npkw, mode="definition", tokens=tokens)["output"]
-    rel = rms(g - ref) / max(rms(ref), 1e-30)
-    print(f"{name} vs definition: rel rms {rel:.4g}", flush=True)
-    assert rel <= 0.05
-    # the reference's own algorithm (64-column requantisation, kernel.py:131-135): per token
-    # and in aggregate, the layer is no further from the fp32 definition than it, within the
-    # factors stated at the top of this file
-    ref64 = olayer.layer_forward(**npkw, mode="emulated", requant_block=64, tokens=tokens)["output"]
-    tok_gpu = np.max(np.abs(g - ref), axis=1)
-    tok_ref = np.max(np.abs(ref64 - ref), axis=1)
-    ratio = tok_gpu / np.maximum(tok_ref, 1e-30)
-    live = tok_ref > 0
-    print(f"{name}: per-token max|gpu - def| / max|ref64 - def|: max {np.max(ratio[live], initial=0):.3f}, "
-          f"median {np.median(ratio[live]) if live.any() else 0:.3f} over {int(live.sum())} tokens", flush=True)
-    bad = tok_gpu > 2.0 * tok_ref + 1.0 / 64
-    assert not bad.any(), f"{name}: {int(bad.sum())} tokens beyond 2 x the reference algorithm's error"
-    e_gpu, e_ref = rms(g - ref), rms(ref64 - ref)
-    print(f"{name}: rms(gpu - definition) {e_gpu:.4g}, rms(reference algorithm - definition) {e_ref:.4g}",
-          flush=True)
-    assert e_gpu <= 1.25 * e_ref
+    _vs_reference_algorithm(g, npkw, tokens, T, name)
     # tokens with no local expert produce exact zeros
     zero = emu["token_nlocal"] == 0
     assert np.all(got[zero] == 0)
@@ -483,6 +497,7 @@ def test_odd_batches_match_oracle(T, offset):
     rel = np.sqrt(np.mean((g - r) ** 2)) / max(np.sqrt(np.mean(r ** 2)), 1e-30)
     print(f"{what} vs emulated oracle: rel rms {rel:.4g}", flush=True)
     assert rel <= 0.01
+    _vs_reference_algorithm(g, npkw, tokens, T, what)
     assert np.all(got[emu["token_nlocal"] == 0] == 0)
 
 
