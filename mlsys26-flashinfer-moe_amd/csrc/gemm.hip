@@ -20,7 +20,9 @@
 //          (below): a work-group per 32 hidden rows across all items, with the tokens'
 //          weighted sums kept in LDS.
 // A wavefront streams its weight rows and the item's activation rows into a register ring
-// (the next K-step in flight while the current one computes). Every K-step is exactly one 128x128 scale block:
+// (the next K-step in flight while the current one computes); GEMM1's and the slice kernel's
+// row-major weights go through a wavefront-private LDS ring instead (stream_accumulate_g1_lds,
+// gemm2_slice_kernel). Every K-step is exactly one 128x128 scale block:
 // one v_mfma_f32_16x16x128_f8f6f4 per fragment pair, then acc += mfma * (s_act * s_w) in
 // fp32 (kernel.py:123-124 and :234).
 //
