@@ -108,6 +108,9 @@ typedef struct moe_fp8_args {
  *   sorted_weight fp32  [N_max]     routing weight of each assignment               (kernel.py:365)
  *   sorted_slot   int32 [N_max]     flat slot t*8+k of each assignment
  *   token_nlocal  int32 [T]         number of local assignments of each token
+ *   slot_rank     int32 [T*8]       internal: the multi-work-group dispatch's stable ranks;
+ *                                   above 256 tokens GEMM1 then reuses it for each bucket
+ *                                   row's output destination (token, or -1 - flat slot)
  *   work_items    int32 [max_items, 4]  GEMM work list (expert, first row, rows,
  *                                   first item of the expert | its item count << 16) (kernel.py:384-407)
  *   counters      int32 [80]        [0] number of work items, [1] N; the rest internal

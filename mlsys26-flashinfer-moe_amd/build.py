@@ -31,6 +31,10 @@ COMMON_FLAGS = [
 # Routing must evaluate its fp32 operation sequence exactly as written.
 PER_FILE_FLAGS = {
     "route_dispatch.hip": ["-ffp-contract=off"],
+    # The tile GEMMs take their next work-list entry with a single-lane atomic whose result is
+    # needed only at the end of the unit's epilogue; the atomic optimizer's rewrite reads the
+    # result back at once, and that wait drains every load in flight.
+    "gemm_tile.hip": ["-mllvm", "-amdgpu-atomic-optimizer-strategy=None"],
 }
 
 

@@ -94,6 +94,7 @@ GemmParams gemm_params(const moe_fp8_args* a, const moe_fp8_layout& L, void* ws)
   p.sorted_weight = at<float>(ws, L.sorted_weight);
   p.sorted_slot = at<int32_t>(ws, L.sorted_slot);
   p.token_nlocal = at<int32_t>(ws, L.token_nlocal);
+  p.row_dest = at<int32_t>(ws, L.slot_rank);
   p.act = at<uint8_t>(ws, L.act);
   p.act_scale = at<float>(ws, L.act_scale);
   p.partial = at<float>(ws, L.partial);

@@ -394,22 +394,42 @@ __device__ __forceinline__ void tile_body(const GemmParams& p, const TileCtx<ROW
         // the first wave of each scale block writes the block's scale
         if ((wb & (S::kQCols / 32 - 1)) == 0 && lane < 16)
           p.act_scale[(size_t)(c.r0 + m) * S::kQBlocks + (c.tile * 128 + 32 * wb) / S::kQCols] = scale;
+        // GEMM2's output destination of the row (the units of tile 0, one wavefront): the
+        // token when it has one local assignment, else -1 - its flat slot
+        if (c.tile == 0 && wb == 0 && lane < 16) {
+          const int pr = c.r0 + m;
+          const int t = p.sorted_token[pr];
+          p.row_dest[pr] = p.token_nlocal[t] == 1 ? t : -1 - p.sorted_slot[pr];
+        }
       }
     }
     __syncthreads();
   } else {
+    // Each row's destination as GEMM1 left it (the token, or -1 - its flat slot) and its routing
+    // weight: two independent loads per row group, all issued before the first store, so that
+    // one round trip covers them and the list entry taken above. Every such wait also waits for
+    // the next unit's prefetched K-steps (vmcnt counts in order); the token's local count, read
+    // here before, was a second dependent round trip. Rows past the item read its first row.
+    int dest[NG > 0 ? NG : 1];
+    float wt[NG > 0 ? NG : 1];
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      const int m = c.m0 + 16 * g + (lane & 15);
+      const int pr = c.r0 + (m < c.rows ? m : 0);
+      dest[g] = p.row_dest[pr];
+      wt[g] = p.sorted_weight[pr];
+    }
+    if (queue != nullptr && threadIdx.x == 0) sh.next = got;
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
       const int m = c.m0 + 16 * g + (lane & 15);
       if (m < c.rows) {
-        const int pr = c.r0 + m;
-        const int t = p.sorted_token[pr];
-        const float wt = p.sorted_weight[pr];
-        const bool direct = p.token_nlocal[t] == 1;
-        const size_t slot = (size_t)p.sorted_slot[pr];
+        const bool direct = dest[g] >= 0;
+        const int t = dest[g];
+        const size_t slot = (size_t)(-1 - dest[g]);
 #pragma unroll
         for (int f = 0; f < 4; ++f) {
-          const v4f val = acc[f][g] * wt;
+          const v4f val = acc[f][g] * wt[g];
           const int h = c.tile * kTileW + 64 * wb + 16 * f + 4 * (lane >> 4);
           if (direct) {
             if (p.out_dtype == MOE_FP8_OUT_BF16)
@@ -424,7 +444,7 @@ __device__ __forceinline__ void tile_body(const GemmParams& p, const TileCtx<ROW
       }
     }
   }
-  if (queue != nullptr && threadIdx.x == 0) sh.next = got;
+  if (G1 && queue != nullptr && threadIdx.x == 0) sh.next = got;
 }
 
 // NG (row groups of this wave's half) as a template argument: instantiations 0..kMaxNG.

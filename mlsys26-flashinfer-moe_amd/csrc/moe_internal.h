@@ -126,6 +126,11 @@ struct GemmParams {
   const float* sorted_weight;
   const int32_t* sorted_slot;
   const int32_t* token_nlocal;
+  // [N_max] output destination of each bucket row on the tile path: the token when it has one
+  // local assignment (its output row is written directly), else -1 - its flat slot (the row
+  // is parked for the combine). The tile GEMM1 writes it into the dispatch's slot_rank array,
+  // which nothing reads after the placement; the tile GEMM2 reads it.
+  int32_t* row_dest;
   uint8_t* act;                // [N_max, 2048]
   float* act_scale;            // [N_max, 2048 / requantisation block]
   float* partial;              // [T*8, 7168]
