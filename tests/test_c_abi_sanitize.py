@@ -8,6 +8,7 @@ layouts across the regime boundaries, every validation error of every entry poin
 texts. Any sanitizer report aborts the program. Every call the program makes is rejected
 before the library looks at the device, so it launches nothing. Leak checking is off: the
 HIP runtime keeps allocations for the process's lifetime."""
+import importlib.util
 import os
 import shutil
 import subprocess
@@ -18,6 +19,11 @@ import pytest
 
 ROOT = Path(__file__).resolve().parent.parent
 CSRC = ROOT / "mlsys26-flashinfer-moe_amd" / "csrc"
+# the product build's per-file compiler flags (its build.py, loaded by path)
+_spec = importlib.util.spec_from_file_location("_moe_fp8_build", CSRC.parent / "build.py")
+_build = importlib.util.module_from_spec(_spec)
+_spec.loader.exec_module(_build)
+PER_FILE_FLAGS = _build.PER_FILE_FLAGS
 HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
 CLANG = "/opt/rocm/llvm/bin/clang"
 HOST_SAN = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
@@ -32,7 +38,7 @@ def sanitized_checker(tmp_path_factory):
     sources = sorted(CSRC.glob("*.hip"))
 
     def compile_one(src):
-        extra = ["-ffp-contract=off"] if src.name == "route_dispatch.hip" else []
+        extra = PER_FILE_FLAGS.get(src.name, [])
         cmd = [HIPCC, "--offload-arch=gfx950", "-O1", "-g", "-std=c++17", "-fPIC",
                "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", *HOST_SAN, *extra,
                "-c", str(src), "-o", str(d / (src.stem + ".o"))]
