@@ -108,9 +108,7 @@ typedef struct moe_fp8_args {
  *   sorted_weight fp32  [N_max]     routing weight of each assignment               (kernel.py:365)
  *   sorted_slot   int32 [N_max]     flat slot t*8+k of each assignment
  *   token_nlocal  int32 [T]         number of local assignments of each token
- *   slot_rank     int32 [T*8]       internal: the multi-work-group dispatch's stable ranks;
- *                                   above 256 tokens GEMM1 then reuses it for each bucket
- *                                   row's output destination (token, or -1 - flat slot)
+ *   slot_rank     int32 [T*8]       internal: the multi-work-group dispatch's stable ranks
  *   work_items    int32 [max_items, 4]  GEMM work list (expert, first row, rows,
  *                                   first item of the expert | its item count << 16) (kernel.py:384-407)
  *   counters      int32 [80]        [0] number of work items, [1] N; the rest internal
@@ -130,6 +128,10 @@ typedef struct moe_fp8_args {
  *                                                                                     (kernel.py:704)
  *   swiglu        fp32  [N_max, 2048]    SwiGLU output before requantisation; only for
  *                                        T <= 256 (0 bytes otherwise)
+ *   row_dest      int32 [N_max]     above 256 tokens, written by the dispatch: GEMM2's output
+ *                                   destination of each bucket row, the token when it has one
+ *                                   local assignment (its output row is written directly),
+ *                                   else -1 - its flat slot (the row is parked in `partial`)
  */
 typedef struct moe_fp8_layout {
   size_t total_bytes;
@@ -149,6 +151,7 @@ typedef struct moe_fp8_layout {
   size_t act_scale;
   size_t partial;
   size_t swiglu;
+  size_t row_dest;
   int32_t num_tokens;
   int32_t max_assignments;   /* N_max = 8*T        */
   int32_t max_work_items;

@@ -106,6 +106,7 @@ class MoeFp8Layout(ctypes.Structure):
         ("act_scale", ctypes.c_size_t),
         ("partial", ctypes.c_size_t),
         ("swiglu", ctypes.c_size_t),
+        ("row_dest", ctypes.c_size_t),
         ("num_tokens", ctypes.c_int32),
         ("max_assignments", ctypes.c_int32),
         ("max_work_items", ctypes.c_int32),

@@ -72,6 +72,7 @@ RouteParams route_params(const moe_fp8_args* a, const moe_fp8_layout& L, void* w
   p.sorted_slot = at<int32_t>(ws, L.sorted_slot);
   p.token_nlocal = at<int32_t>(ws, L.token_nlocal);
   p.slot_rank = at<int32_t>(ws, L.slot_rank);
+  p.row_dest = at<int32_t>(ws, L.row_dest);
   p.block_count = at<int32_t>(ws, L.block_count);
   p.work_items = at<int32_t>(ws, L.work_items);
   p.counters = at<int32_t>(ws, L.counters);
@@ -94,7 +95,7 @@ GemmParams gemm_params(const moe_fp8_args* a, const moe_fp8_layout& L, void* ws)
   p.sorted_weight = at<float>(ws, L.sorted_weight);
   p.sorted_slot = at<int32_t>(ws, L.sorted_slot);
   p.token_nlocal = at<int32_t>(ws, L.token_nlocal);
-  p.row_dest = at<int32_t>(ws, L.slot_rank);
+  p.row_dest = at<int32_t>(ws, L.row_dest);
   p.act = at<uint8_t>(ws, L.act);
   p.act_scale = at<float>(ws, L.act_scale);
   p.partial = at<float>(ws, L.partial);
@@ -157,6 +158,7 @@ int compute_layout(int32_t T, moe_fp8_layout* out) {
   L.act_scale = take(nmax * (kInter / 64) * sizeof(float));
   L.partial = take(rpi == 16 ? 0 : t * kTopK * kHidden * sizeof(float));
   L.swiglu = take(rpi <= 32 ? nmax * kInter * sizeof(float) : 0);
+  L.row_dest = take(nmax * sizeof(int32_t));
   L.total_bytes = off;
   // The streaming batches' largest workspace (with its fp32 SwiGLU rows) exceeds the first tile
   // batches' own: every tile batch reserves at least that much, so that the size is

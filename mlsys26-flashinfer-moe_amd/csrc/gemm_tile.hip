@@ -394,22 +394,16 @@ __device__ __forceinline__ void tile_body(const GemmParams& p, const TileCtx<ROW
         // the first wave of each scale block writes the block's scale
         if ((wb & (S::kQCols / 32 - 1)) == 0 && lane < 16)
           p.act_scale[(size_t)(c.r0 + m) * S::kQBlocks + (c.tile * 128 + 32 * wb) / S::kQCols] = scale;
-        // GEMM2's output destination of the row (the units of tile 0, one wavefront): the
-        // token when it has one local assignment, else -1 - its flat slot
-        if (c.tile == 0 && wb == 0 && lane < 16) {
-          const int pr = c.r0 + m;
-          const int t = p.sorted_token[pr];
-          p.row_dest[pr] = p.token_nlocal[t] == 1 ? t : -1 - p.sorted_slot[pr];
-        }
       }
     }
     __syncthreads();
   } else {
-    // Each row's destination as GEMM1 left it (the token, or -1 - its flat slot) and its routing
-    // weight: two independent loads per row group, all issued before the first store, so that
-    // one round trip covers them and the list entry taken above. Every such wait also waits for
-    // the next unit's prefetched K-steps (vmcnt counts in order); the token's local count, read
-    // here before, was a second dependent round trip. Rows past the item read its first row.
+    // Each row's destination as the dispatch wrote it (the token, or -1 - its flat slot) and its
+    // routing weight: two independent loads per row group, all issued before the first store, so
+    // that one round trip covers them and the list entry taken above (a wait also waits for the
+    // next unit's prefetched K-steps: vmcnt counts in order; deriving the destination here from
+    // the token's local count took a second, dependent round trip). Rows past the item read its
+    // first row.
     int dest[NG > 0 ? NG : 1];
     float wt[NG > 0 ? NG : 1];
 #pragma unroll

@@ -106,6 +106,9 @@ struct RouteParams {
   int32_t* sorted_slot;
   int32_t* token_nlocal;
   int32_t* slot_rank;
+  // [N_max] output destination of each bucket row for the tile GEMM2 (place_kernel): the token
+  // when it has one local assignment, else -1 - its flat slot
+  int32_t* row_dest;
   int32_t* block_count;  // [nblocks, 32] expert histogram of each routing work-group
   int32_t* work_items;   // [max_items, 4]
   int32_t* counters;
@@ -126,11 +129,10 @@ struct GemmParams {
   const float* sorted_weight;
   const int32_t* sorted_slot;
   const int32_t* token_nlocal;
-  // [N_max] output destination of each bucket row on the tile path: the token when it has one
-  // local assignment (its output row is written directly), else -1 - its flat slot (the row
-  // is parked for the combine). The tile GEMM1 writes it into the dispatch's slot_rank array,
-  // which nothing reads after the placement; the tile GEMM2 reads it.
-  int32_t* row_dest;
+  // [N_max] output destination of each bucket row on the tile path, as the dispatch wrote it:
+  // the token when it has one local assignment (its output row is written directly), else
+  // -1 - its flat slot (the row is parked for the combine)
+  const int32_t* row_dest;
   uint8_t* act;                // [N_max, 2048]
   float* act_scale;            // [N_max, 2048 / requantisation block]
   float* partial;              // [T*8, 7168]

@@ -551,6 +551,11 @@ __global__ __launch_bounds__(kPlaceThreads) void place_kernel(RouteParams p) {
   const int le = has_slot ? local_of(p.topk_ids[s], p.offset) : -1;
   const int rank = le >= 0 ? p.slot_rank[s] : 0;
   const float w = le >= 0 ? p.topk_w[s] : 0.f;
+  // the token's local assignments (its 8 slots are 8 aligned lanes of this wavefront) decide
+  // where GEMM2 sends the row: the token's output row if it has one, else its parked row
+  const uint64_t lm = __ballot(le >= 0);
+  const int tok = s / kTopK;
+  const int dest = __popcll((lm >> (lane_id() & 56)) & 0xFFull) == 1 ? tok : -1 - s;
 
   if constexpr (SCANNED) {
     if (tid < kExpertsLocal) s_prefix[tid] = p.block_count[b * kExpertsLocal + tid];
@@ -558,9 +563,10 @@ __global__ __launch_bounds__(kPlaceThreads) void place_kernel(RouteParams p) {
     __syncthreads();
     if (le < 0) return;
     const int pos = s_start[le] + s_prefix[le] + rank;
-    p.sorted_token[pos] = s / kTopK;
+    p.sorted_token[pos] = tok;
     p.sorted_weight[pos] = w;
     p.sorted_slot[pos] = s;
+    p.row_dest[pos] = dest;
     return;
   }
   const int e = tid % kExpertsLocal, j = tid / kExpertsLocal;
@@ -605,9 +611,10 @@ __global__ __launch_bounds__(kPlaceThreads) void place_kernel(RouteParams p) {
   __syncthreads();
   if (le < 0) return;
   const int pos = s_start[le] + s_prefix[le] + rank;
-  p.sorted_token[pos] = s / kTopK;
+  p.sorted_token[pos] = tok;
   p.sorted_weight[pos] = w;
   p.sorted_slot[pos] = s;
+  p.row_dest[pos] = dest;
 }
 
 // Per-expert exclusive prefix of the routing work-groups' histograms, for batches of more than

@@ -46,7 +46,7 @@ static void valid_args(moe_fp8_args* a, int32_t T) {
 /* The layout's arrays: 256-byte aligned, inside the total, in order and not overlapping. */
 static void check_layout(int32_t T) {
   moe_fp8_layout L;
-  size_t off[16];
+  size_t off[17];
   int n = 0, i;
   int rc = moe_fp8_workspace_layout(T, &L);
   CHECK(rc == MOE_FP8_OK);
@@ -57,7 +57,7 @@ static void check_layout(int32_t T) {
   off[n++] = L.sorted_weight; off[n++] = L.sorted_slot; off[n++] = L.token_nlocal;
   off[n++] = L.slot_rank;    off[n++] = L.block_count;  off[n++] = L.work_items;
   off[n++] = L.act;          off[n++] = L.act_scale;    off[n++] = L.partial;
-  off[n++] = L.swiglu;
+  off[n++] = L.swiglu;       off[n++] = L.row_dest;
   for (i = 0; i < n; ++i) {
     CHECK(off[i] % 256 == 0);
     CHECK(off[i] <= L.total_bytes);

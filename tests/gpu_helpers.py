@@ -109,6 +109,12 @@ def check_dispatch(ws: Workspace, ids: np.ndarray, w: np.ndarray, offset: int, T
     assert np.array_equal(read(ws, "sorted_weight", torch.float32, n).view(np.uint32),
                           d["sorted_weight"].view(np.uint32))
     assert np.array_equal(read(ws, "token_nlocal", torch.int32, T), d["token_nlocal"])
+    if T > 256:
+        # the multi-work-group dispatch also leaves GEMM2's destination of every bucket row: the
+        # token if it has one local assignment, else -1 - the row's flat slot
+        st, ss = d["sorted_token"], d["sorted_slot"]
+        want = np.where(d["token_nlocal"][st] == 1, st, -1 - ss).astype(np.int32)
+        assert np.array_equal(read(ws, "row_dest", torch.int32, n), want)
     rpi = int(ws.layout.rows_per_item)
     items = odsp.work_items(d["expert_count"], d["expert_start"], rpi)
     assert c[0] == len(items)

@@ -40,7 +40,7 @@ def test_constants_match_header(pkg):
 def test_struct_sizes(pkg):
     # 14 fields with natural alignment on x86-64
     assert ctypes.sizeof(pkg._lib.MoeFp8Args) == 104
-    assert ctypes.sizeof(pkg._lib.MoeFp8Layout) == 17 * 8 + 8 * 4
+    assert ctypes.sizeof(pkg._lib.MoeFp8Layout) == 18 * 8 + 8 * 4
 
 
 @pytest.mark.parametrize("T", [0, 1, 15, 16, 17, 64, 257, 1024, 4096, 8192, 65536])
@@ -63,7 +63,7 @@ def test_layout_consistent(pkg, T):
         ("block_count", 4 * 32 * L.route_blocks), ("work_items", 16 * L.max_work_items),
         ("counters", 4 * 80), ("act", 8 * T * 2048), ("act_scale", 4 * 8 * T * 2048 // 64),
         ("partial", 0 if decode else 4 * 8 * T * 7168),
-        ("swiglu", 4 * 8 * T * 2048 if L.rows_per_item <= 32 else 0),
+        ("swiglu", 4 * 8 * T * 2048 if L.rows_per_item <= 32 else 0), ("row_dest", 4 * 8 * T),
     ]
     spans = sorted((getattr(L, n), getattr(L, n) + b, n) for n, b in arrays)
     for (a0, a1, an), (b0, b1, bn) in zip(spans, spans[1:]):

@@ -318,6 +318,38 @@ def test_tile_stage_repeated(name):
     assert torch.equal(whole.view(torch.int16), out.view(torch.int16)), "staged and whole-layer runs differ"
 
 
+@pytest.mark.parametrize("name", ["t1024_off64", "t4096_skew"])
+def test_gemm2_stage_on_a_written_intermediate(name):
+    """Above 256 tokens the GEMM2 stage needs only the dispatch and the fp8 intermediate: a
+    fresh workspace given the dispatch and an intermediate written by the caller (GEMM1 never
+    run there) produces the whole layer's output bit for bit."""
+    gh = _gh()
+    kw, _ = _workload(name)
+    T = kw["routing_logits"].shape[0]
+    print(f"gemm2 stage on a written intermediate {name} T={T}", flush=True)
+    whole = _run_full(kw)
+    dev = kw["routing_logits"].device
+    ws = gh.new_workspace(T, dev)
+    assert ws.layout.rows_per_item > 32
+    out1 = torch.empty((T, 7168), dtype=torch.bfloat16, device=dev)   # not written by these stages
+    args = gh.make_args(**kw, output=out1)
+    gh.route_dispatch(args, ws)
+    gh.gemm1(args, ws)
+    n = int(gh.counters(ws)[1])
+    nb = 2048 // int(ws.layout.requant_block)
+    act = gh.read(ws, "act", torch.uint8, n * 2048)
+    sc = gh.read(ws, "act_scale", torch.float32, n * nb)
+    out = torch.full((T, 7168), float("nan"), dtype=torch.bfloat16, device=dev)
+    args2 = gh.make_args(**kw, output=out)
+    ws2 = gh.new_workspace(T, dev)
+    gh.route_dispatch(args2, ws2)
+    gh.write(ws2, "act", act)
+    gh.write(ws2, "act_scale", sc)
+    gh.gemm2_combine(args2, ws2)
+    torch.cuda.synchronize()
+    assert torch.equal(whole.view(torch.int16), out.view(torch.int16)), "GEMM2 stage differs from the whole layer"
+
+
 @pytest.mark.parametrize("name", ["t64", "t1024_off64", "t8192", "t4096_skew"])
 def test_deterministic_and_fp32_output(name):
     """Two calls give the same bits, also where the tile kernels' work-groups take their units
