@@ -2,6 +2,7 @@
 // run() in kernel.py:562-729 is the interface these entry points replace.
 #include <string.h>
 
+#include <atomic>
 #include <mutex>
 
 #include "moe_internal.h"
@@ -14,16 +15,18 @@ constexpr size_t kAlign = 256;
 inline size_t align_up(size_t x) { return (x + kAlign - 1) & ~(kAlign - 1); }
 
 int check_device() {
-  static int verdict[64] = {0};  // 0 unknown, 1 ok, -1 wrong arch
+  // per device: 0 unknown, 1 gfx950, -1 another GPU (concurrent first calls store the same)
+  static std::atomic<int> verdict[64] = {};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0) return MOE_FP8_EDEVICE;
-  if (dev >= 64) return MOE_FP8_OK;
-  if (verdict[dev] == 0) {
+  int v = dev < 64 ? verdict[dev].load(std::memory_order_relaxed) : 0;
+  if (v == 0) {
     hipDeviceProp_t prop;
     if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return MOE_FP8_EDEVICE;
-    verdict[dev] = strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 1 : -1;
+    v = strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 1 : -1;
+    if (dev < 64) verdict[dev].store(v, std::memory_order_relaxed);   // devices past 64: uncached
   }
-  return verdict[dev] == 1 ? MOE_FP8_OK : MOE_FP8_EDEVICE;
+  return v == 1 ? MOE_FP8_OK : MOE_FP8_EDEVICE;
 }
 
 int check_args(const moe_fp8_args* a, bool need_routing, void* ws, size_t ws_bytes,

@@ -30,6 +30,7 @@
 // [16g, 16g+16) and [64+16g, 64+16g+16) of its row (weights and activations alike, so the
 // dot products are unchanged). Each 16-byte load instruction of a wavefront then reads
 // whole 64-byte segments of 16 rows.
+#include <atomic>
 #include <type_traits>
 
 #include "moe_internal.h"
@@ -925,27 +926,29 @@ __global__ __launch_bounds__(256) void combine_kernel(GemmParams p) {
   }
 }
 
+// Host-side caches of device facts are atomics: concurrent first calls from several host
+// threads each compute the same value and store it.
 int num_cus() {
-  static int cached[64] = {0};
+  static std::atomic<int> cached[64] = {};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (!cached[dev]) {
-    int n = 0;
+  int n = cached[dev].load(std::memory_order_relaxed);
+  if (!n) {
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cached[dev] = n;
+    cached[dev].store(n, std::memory_order_relaxed);
   }
-  return cached[dev];
+  return n;
 }
 
 // Work-groups of `kernel` that one CU holds at once (cached per kernel; 1 if unknown).
 template <typename K>
-int resident_per_cu(K kernel, int& cache) {
-  if (!cache) {
-    int n = 0;
+int resident_per_cu(K kernel, std::atomic<int>& cache) {
+  int n = cache.load(std::memory_order_relaxed);
+  if (!n) {
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, kStreamWaves * 64, 0) != hipSuccess || n <= 0) n = 1;
-    cache = n;
+    cache.store(n, std::memory_order_relaxed);
   }
-  return cache;
+  return n;
 }
 
 // One wave of resident work-groups: every work-group starts at once, and the round-robin
@@ -953,7 +956,7 @@ int resident_per_cu(K kernel, int& cache) {
 // would run at a fraction of the occupancy).
 template <int KIND, int MAXNG, bool PACKED = false>
 hipError_t launch_stream_ng(const GemmParams& p, hipStream_t s) {
-  static int occ = 0;
+  static std::atomic<int> occ{0};
   const auto kernel = gemm_stream_kernel<KIND, MAXNG, PACKED>;
   const int max_units = p.max_items * StreamShape<KIND>::kSlices;
   int grid = num_cus() * resident_per_cu(kernel, occ);
@@ -1019,7 +1022,7 @@ hipError_t launch_gemm1(const GemmParams& p, int rows_per_item, bool packed, hip
 
 hipError_t launch_gemm1_dispatch(const GemmParams& p, const RouteParams& rp, bool packed, hipStream_t s) {
   // one wave of resident work-groups of the instance launched (each has its own occupancy)
-  static int occ_rows = 0, occ_packed = 0;
+  static std::atomic<int> occ_rows{0}, occ_packed{0};
   if (p.T <= 0 || p.T > kFusedDispatchTokens || rp.rows_per_item != kFusedItemRows) return hipErrorInvalidValue;
   int grid = num_cus() * (packed ? resident_per_cu(gemm1_stream_dispatch_kernel<true>, occ_packed)
                                  : resident_per_cu(gemm1_stream_dispatch_kernel<false>, occ_rows));

@@ -54,6 +54,8 @@
 //   Static blocks (GEMM2 with items of up to 160 rows): the units are dealt to the 8 XCDs in
 //          contiguous blocks, a work-group's units fixed in advance (the lists measured 253
 //          against 247 us at T=8192 and 573 against 552 on the skewed batch).
+#include <atomic>
+
 #include "moe_internal.h"
 #include "moe_device.h"
 
@@ -660,16 +662,17 @@ __global__ __launch_bounds__(kTileWaves * 64, 1) void gemm_tile_kernel(GemmParam
   }
 }
 
+// CU count per device (an atomic: concurrent first calls store the same value)
 int num_cus_tile() {
-  static int cached[64] = {0};
+  static std::atomic<int> cached[64] = {};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (!cached[dev]) {
-    int n = 0;
+  int n = cached[dev].load(std::memory_order_relaxed);
+  if (!n) {
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cached[dev] = n;
+    cached[dev].store(n, std::memory_order_relaxed);
   }
-  return cached[dev];
+  return n;
 }
 
 template <bool G1, int ROWS>
