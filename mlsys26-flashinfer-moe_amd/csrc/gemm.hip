@@ -17,7 +17,7 @@
 //          to its output row, the others park v in `partial` by flat slot for
 //          combine_kernel (the reference adds with fp32 atomics, kernel.py:246-250).
 //          Up to 64 tokens GEMM2 and the combine are one kernel instead, gemm2_slice_kernel
-//          (below): a work-group per 32 hidden rows across all items, with the tokens'
+//          (below): a work-group per 28 hidden rows across all items, with the tokens'
 //          weighted sums kept in LDS.
 // A wavefront streams its weight rows and the item's activation rows into a register ring
 // (the next K-step in flight while the current one computes); GEMM1's and the slice kernel's
