@@ -363,6 +363,34 @@ def test_deterministic_and_fp32_output(name):
     assert torch.equal(f.to(torch.bfloat16).view(torch.int16), a.view(torch.int16))
 
 
+def test_two_streams_at_once():
+    """run() on two streams at the same time, a decode batch on one and a tile-path batch on
+    the other, three calls each: every output equals the call's output alone, bit for bit (each
+    stream has its own workspace; the library keeps no other state between calls)."""
+    gh = _gh()
+    dev = torch.device("cuda:0")
+    kw_a, _ = _workload("t64")
+    kw_b, _ = _workload("t1024_off64")
+    print("two streams: t64 and t1024_off64, 3 calls each", flush=True)
+    ref_a, ref_b = _run_full(kw_a), _run_full(kw_b)
+    cur = torch.cuda.current_stream(dev)
+    outs = {n: [torch.full((kw["routing_logits"].shape[0], 7168), float("nan"), dtype=torch.bfloat16, device=dev)
+                for _ in range(3)] for n, kw in (("a", kw_a), ("b", kw_b))}
+    streams = {"a": torch.cuda.Stream(dev), "b": torch.cuda.Stream(dev)}
+    for s in streams.values():
+        s.wait_stream(cur)   # inputs and outputs were written on the current stream
+    for i in range(3):
+        for n, kw in (("a", kw_a), ("b", kw_b)):
+            with torch.cuda.stream(streams[n]):
+                gh.pkg.run(**kw, output=outs[n][i])
+    for s in streams.values():
+        cur.wait_stream(s)
+    torch.cuda.synchronize()
+    for n, ref in (("a", ref_a), ("b", ref_b)):
+        for i, o in enumerate(outs[n]):
+            assert torch.equal(o.view(torch.int16), ref.view(torch.int16)), f"stream {n} call {i} differs"
+
+
 def test_cpu_output_and_inputs_are_moved():
     gh = _gh()
     kw, _ = _workload("t16")
