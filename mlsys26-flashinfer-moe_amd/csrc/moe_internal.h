@@ -68,6 +68,9 @@ constexpr int kTileItemRowsLarge = 160;
 // Batches up to kStreamMaxTokens run the wavefront-granular streaming GEMMs (items of 16 or
 // 32 rows), larger ones the tile GEMMs.
 constexpr int kStreamMaxTokens = 256;
+// The tile GEMM2 reads each bucket row's destination (row_dest), which only place_kernel
+// writes: every batch of the tile path takes the multi-work-group dispatch.
+static_assert(kSinglePassTokens <= kStreamMaxTokens, "tile-path batches are dispatched by place_kernel");
 
 inline int rows_per_item_for(int T) {
   if (T <= 64) return 16;
