@@ -10,7 +10,11 @@
  * Every entry point is stream-ordered on the hipStream_t it is given, performs no
  * host<->device synchronisation and allocates no memory: all temporaries live in a
  * caller-owned workspace of moe_fp8_workspace_bytes(T) bytes. Pointers are device
- * pointers to contiguous row-major buffers. Return value: 0 on success, a negative
+ * pointers to contiguous row-major buffers, aligned for the widest access the kernels make to
+ * them (MOE_FP8_EALIGN otherwise): 16 bytes for the logits, hidden states, weights, packed
+ * weights, an fp32 output and the quantiser's input; 8 for a bf16 output and the quantiser's
+ * fp8 output; 4 for scales and an fp32 bias; 2 for a bf16 or fp16 bias; 256 for the workspace
+ * (every allocation of hipMalloc or torch qualifies). Return value: 0 on success, a negative
  * MOE_FP8_E* code otherwise (moe_fp8_strerror() gives the text). Arguments are checked
  * before anything is launched, so on every error but MOE_FP8_ELAUNCH nothing has been
  * launched; MOE_FP8_ELAUNCH reports a launch that HIP rejected, possibly after earlier
@@ -72,6 +76,7 @@ extern "C" {
 #define MOE_FP8_EINVAL_HIDDEN_DTYPE -8 /* hidden_dtype of moe_fp8_quantize_hidden unknown */
 #define MOE_FP8_ESTATIC_TOKENS     -9  /* num_tokens > MOE_FP8_STATIC_MAX_TOKENS (moe_fp8_run_static) */
 #define MOE_FP8_EPACKED           -10  /* packed weights NULL or smaller than moe_fp8_packed_weights_bytes() */
+#define MOE_FP8_EALIGN            -11  /* a pointer is not aligned as the kernels read or write it (above) */
 
 /* Largest num_tokens accepted: keeps every flat index (T*8*7168) inside int64 and
  * the per-token slot index inside int32. */

@@ -41,6 +41,7 @@ EDEVICE = -7
 EINVAL_HIDDEN_DTYPE = -8
 ESTATIC_TOKENS = -9
 EPACKED = -10
+EALIGN = -11
 STATIC_MAX_TOKENS = 64
 PACKED_MAX_TOKENS = 256
 STATIC_SCRATCH_BYTES = 6 << 20

@@ -29,6 +29,21 @@ int check_device() {
   return v == 1 ? MOE_FP8_OK : MOE_FP8_EDEVICE;
 }
 
+// Alignment of a pointer to the widest access the kernels make through it (16-byte vector
+// loads and DMAs of the logits, hidden rows, weights and packed weights; 16- or 8-byte output
+// stores; 4-byte scale loads; the 256-byte aligned workspace layout).
+inline bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
+constexpr uintptr_t kWorkspaceAlign = 256;
+
+bool args_aligned(const moe_fp8_args* a, bool need_routing) {
+  if (need_routing &&
+      (!aligned(a->routing_logits, 16) || !aligned(a->routing_bias, a->routing_bias_dtype == MOE_FP8_BIAS_F32 ? 4 : 2)))
+    return false;
+  return aligned(a->hidden_states, 16) && aligned(a->hidden_states_scale, 4) && aligned(a->gemm1_weights, 16) &&
+         aligned(a->gemm1_weights_scale, 4) && aligned(a->gemm2_weights, 16) && aligned(a->gemm2_weights_scale, 4) &&
+         aligned(a->output, a->output_dtype == MOE_FP8_OUT_F32 ? 16 : 8);
+}
+
 int check_args(const moe_fp8_args* a, bool need_routing, void* ws, size_t ws_bytes,
                moe_fp8_layout* L) {
   if (!a) return MOE_FP8_EINVAL_POINTER;
@@ -43,7 +58,9 @@ int check_args(const moe_fp8_args* a, bool need_routing, void* ws, size_t ws_byt
     return MOE_FP8_EINVAL_BIAS_DTYPE;
   if (a->output_dtype != MOE_FP8_OUT_BF16 && a->output_dtype != MOE_FP8_OUT_F32)
     return MOE_FP8_EINVAL_OUT_DTYPE;
+  if (!args_aligned(a, need_routing)) return MOE_FP8_EALIGN;
   if (!ws || ws_bytes < L->total_bytes) return MOE_FP8_EWORKSPACE;
+  if (!aligned(ws, kWorkspaceAlign)) return MOE_FP8_EALIGN;
   return check_device();
 }
 
@@ -268,6 +285,7 @@ int moe_fp8_workspace_layout(int32_t num_tokens, moe_fp8_layout* layout) {
 
 int moe_fp8_workspace_init(void* workspace, size_t workspace_bytes, hipStream_t stream) {
   if (!workspace || workspace_bytes < kNumCounters * sizeof(int32_t)) return MOE_FP8_EWORKSPACE;
+  if (!aligned(workspace, kWorkspaceAlign)) return MOE_FP8_EALIGN;
   return launch_clear_control(static_cast<int32_t*>(workspace), stream) == hipSuccess ? MOE_FP8_OK
                                                                                       : MOE_FP8_ELAUNCH;
 }
@@ -314,6 +332,7 @@ int moe_fp8_run_profiled(const moe_fp8_args* args, const void* packed, size_t pa
                          size_t workspace_bytes, hipStream_t stream, hipEvent_t events[4]) {
   if (!events || !events[0] || !events[1] || !events[2] || !events[3]) return MOE_FP8_EINVAL_POINTER;
   if (packed && packed_bytes < packed_weights_bytes()) return MOE_FP8_EPACKED;
+  if (!aligned(packed, 16)) return MOE_FP8_EALIGN;
   return run_layer(args, workspace, workspace_bytes, stream, events, static_cast<const uint8_t*>(packed));
 }
 
@@ -322,6 +341,8 @@ size_t moe_fp8_packed_weights_bytes(void) { return packed_weights_bytes(); }
 int moe_fp8_pack_weights(const moe_fp8_args* args, void* packed, size_t packed_bytes, hipStream_t stream) {
   if (!args || !args->gemm1_weights || !args->gemm2_weights) return MOE_FP8_EINVAL_POINTER;
   if (!packed || packed_bytes < packed_weights_bytes()) return MOE_FP8_EPACKED;
+  if (!aligned(args->gemm1_weights, 16) || !aligned(args->gemm2_weights, 16) || !aligned(packed, 16))
+    return MOE_FP8_EALIGN;
   const int rc = check_device();
   if (rc != MOE_FP8_OK) return rc;
   return launch_pack_weights(args->gemm1_weights, args->gemm2_weights, static_cast<uint8_t*>(packed), stream) ==
@@ -333,6 +354,7 @@ int moe_fp8_pack_weights(const moe_fp8_args* args, void* packed, size_t packed_b
 int moe_fp8_run_packed(const moe_fp8_args* args, const void* packed, size_t packed_bytes, void* workspace,
                        size_t workspace_bytes, hipStream_t stream) {
   if (!packed || packed_bytes < packed_weights_bytes()) return MOE_FP8_EPACKED;
+  if (!aligned(packed, 16)) return MOE_FP8_EALIGN;
   return run_layer(args, workspace, workspace_bytes, stream, nullptr, static_cast<const uint8_t*>(packed));
 }
 
@@ -345,7 +367,7 @@ int moe_fp8_run_static(const moe_fp8_args* args, hipStream_t stream) {
   // than MOE_FP8_ELAUNCH never leaves a launch behind (the stand-in pointer is only tested
   // against null here; run_layer checks again with the real address)
   moe_fp8_layout L;
-  static uint8_t stand_in;
+  alignas(kWorkspaceAlign) static uint8_t stand_in;
   int rc = check_args(args, true, &stand_in, MOE_FP8_STATIC_SCRATCH_BYTES, &L);
   if (rc != MOE_FP8_OK) return rc;
   void* ws = nullptr;
@@ -360,6 +382,7 @@ int moe_fp8_quantize_hidden(const void* hidden, int32_t hidden_dtype, int32_t nu
   if (num_tokens == 0) return MOE_FP8_OK;
   if (!hidden || !hidden_fp8 || !hidden_scale) return MOE_FP8_EINVAL_POINTER;
   if (hidden_dtype < MOE_FP8_HIDDEN_F32 || hidden_dtype > MOE_FP8_HIDDEN_F16) return MOE_FP8_EINVAL_HIDDEN_DTYPE;
+  if (!aligned(hidden, 16) || !aligned(hidden_fp8, 8) || !aligned(hidden_scale, 4)) return MOE_FP8_EALIGN;
   const int rc = check_device();
   if (rc != MOE_FP8_OK) return rc;
   return launch_quantize_hidden(hidden, hidden_dtype, num_tokens, static_cast<uint8_t*>(hidden_fp8), hidden_scale,
@@ -380,6 +403,10 @@ const char* moe_fp8_strerror(int code) {
     case MOE_FP8_EDEVICE: return "the current HIP device is not a gfx950 (MI355X) GPU";
     case MOE_FP8_EINVAL_HIDDEN_DTYPE: return "hidden_dtype must be MOE_FP8_HIDDEN_F32, _BF16 or _F16";
     case MOE_FP8_EPACKED: return "packed weights are NULL or smaller than moe_fp8_packed_weights_bytes()";
+    case MOE_FP8_EALIGN:
+      return "a pointer is not aligned as the kernels access it (16 bytes: logits, hidden states, weights, packed "
+             "weights, fp32 output, quantiser input; 8: bf16 output, quantiser output; 4: scales, fp32 bias; "
+             "2: bf16/fp16 bias; 256: workspace)";
     case MOE_FP8_ESTATIC_TOKENS:
       return "num_tokens exceeds MOE_FP8_STATIC_MAX_TOKENS (64), the largest batch moe_fp8_run_static's "
              "built-in workspace holds; use moe_fp8_run with a caller workspace";

@@ -38,6 +38,12 @@ def _ensure_cuda(*tensors) -> torch.device:
     return torch.device("cuda")
 
 
+def _aligned(t: torch.Tensor, n: int) -> torch.Tensor:
+    """t itself when its data is n-byte aligned (the kernels' widest access to it), else a copy
+    (a fresh allocation is always aligned). The reference takes any tensor; this keeps that."""
+    return t if t.data_ptr() % n == 0 else t.clone()
+
+
 def validate(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
              gemm1_weights_scale, gemm2_weights, gemm2_weights_scale) -> int:
     """The dtype and shape checks of kernel.py:591-607; returns T."""
@@ -344,7 +350,7 @@ def pack_weights(gemm1_weights: torch.Tensor, gemm2_weights: torch.Tensor) -> to
         raise RuntimeError("pack_weights needs both weight tensors on one GPU")
     dev = gemm1_weights.device
     lib = _lib.load()
-    w13, w2 = gemm1_weights.contiguous(), gemm2_weights.contiguous()
+    w13, w2 = _aligned(gemm1_weights.contiguous(), 16), _aligned(gemm2_weights.contiguous(), 16)
     packed = torch.empty(_lib.packed_weights_bytes(), dtype=torch.uint8, device=dev)
     args = _lib.MoeFp8Args()
     args.gemm1_weights = w13.data_ptr()
@@ -379,21 +385,21 @@ def _run(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1
                           gemm1_weights, gemm1_weights_scale, gemm2_weights, gemm2_weights_scale)
     lib = _lib.load()
 
-    logits = _check_cuda_and_move(routing_logits, device).contiguous()
-    bias = _check_cuda_and_move(routing_bias, device).contiguous()
-    hidden = _check_cuda_and_move(hidden_states, device).contiguous()
-    hidden_scale = _check_cuda_and_move(hidden_states_scale, device).contiguous()
-    w13 = _check_cuda_and_move(gemm1_weights, device).contiguous()
-    w13_scale = _check_cuda_and_move(gemm1_weights_scale, device).contiguous()
-    w2 = _check_cuda_and_move(gemm2_weights, device).contiguous()
-    w2_scale = _check_cuda_and_move(gemm2_weights_scale, device).contiguous()
+    logits = _aligned(_check_cuda_and_move(routing_logits, device).contiguous(), 16)
+    bias = _aligned(_check_cuda_and_move(routing_bias, device).contiguous(), 4)
+    hidden = _aligned(_check_cuda_and_move(hidden_states, device).contiguous(), 16)
+    hidden_scale = _aligned(_check_cuda_and_move(hidden_states_scale, device).contiguous(), 4)
+    w13 = _aligned(_check_cuda_and_move(gemm1_weights, device).contiguous(), 16)
+    w13_scale = _aligned(_check_cuda_and_move(gemm1_weights_scale, device).contiguous(), 4)
+    w2 = _aligned(_check_cuda_and_move(gemm2_weights, device).contiguous(), 16)
+    w2_scale = _aligned(_check_cuda_and_move(gemm2_weights_scale, device).contiguous(), 4)
     dev = logits.device
     for t in (bias, hidden, hidden_scale, w13, w13_scale, w2, w2_scale):
         if t.device != dev:
             raise RuntimeError(f"all inputs must be on one device; got {t.device} and {dev}")
 
     direct = output.is_cuda and output.device == dev and output.is_contiguous() and \
-        output.dtype in (torch.bfloat16, torch.float32)
+        output.dtype in (torch.bfloat16, torch.float32) and output.data_ptr() % 16 == 0
     dst = output if direct else torch.empty((T, HIDDEN), dtype=torch.bfloat16, device=dev)
     if T == 0:
         return None
@@ -433,7 +439,7 @@ def quantize_hidden(hidden: torch.Tensor, out: torch.Tensor | None = None,
     assert hidden.dtype in _HIDDEN_CODES, "hidden must be float32, bfloat16 or float16"
     assert hidden.dim() == 2 and hidden.shape[1] == HIDDEN, "hidden must be [T, 7168]"
     device = _ensure_cuda(hidden, out, out_scale)
-    x = _check_cuda_and_move(hidden, device).contiguous()
+    x = _aligned(_check_cuda_and_move(hidden, device).contiguous(), 16)
     T = int(x.shape[0])
     if out is None:
         out = torch.empty((T, HIDDEN), dtype=torch.float8_e4m3fn, device=x.device)
@@ -447,8 +453,16 @@ def quantize_hidden(hidden: torch.Tensor, out: torch.Tensor | None = None,
             raise RuntimeError("out and out_scale must be contiguous tensors on the input's device")
     if T == 0:
         return out, out_scale
+    # destinations the kernel cannot store to directly (8-byte fp8 stores, 4-byte scale stores)
+    # are written through aligned temporaries
+    q = out if out.data_ptr() % 8 == 0 else torch.empty_like(out)
+    qs = out_scale if out_scale.data_ptr() % 4 == 0 else torch.empty_like(out_scale)
     with torch.cuda.device(x.device):
         stream = torch.cuda.current_stream(x.device).cuda_stream
-        _lib.check(_lib.load().moe_fp8_quantize_hidden(x.data_ptr(), _HIDDEN_CODES[x.dtype], T, out.data_ptr(),
-                                                       out_scale.data_ptr(), stream), "moe_fp8_quantize_hidden")
+        _lib.check(_lib.load().moe_fp8_quantize_hidden(x.data_ptr(), _HIDDEN_CODES[x.dtype], T, q.data_ptr(),
+                                                       qs.data_ptr(), stream), "moe_fp8_quantize_hidden")
+    if q is not out:
+        out.copy_(q)
+    if qs is not out_scale:
+        out_scale.copy_(qs)
     return out, out_scale

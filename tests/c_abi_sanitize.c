@@ -107,6 +107,20 @@ static void check_entry_points(int32_t T, void* ws, size_t ws_bytes) {
   valid_args(&a, T);
   a.output_dtype = 7;
   CHECK(moe_fp8_run(&a, ws, ws_bytes, NULL) == MOE_FP8_EINVAL_OUT_DTYPE);
+  /* a pointer off its alignment (16: hidden states; 4: scales; 8: bf16 output), a workspace off 256 */
+  valid_args(&a, T);
+  a.hidden_states = fake(0x3008);
+  CHECK(moe_fp8_run(&a, ws, ws_bytes, NULL) == MOE_FP8_EALIGN);
+  CHECK(moe_fp8_gemm2_combine(&a, ws, ws_bytes, NULL) == MOE_FP8_EALIGN);
+  valid_args(&a, T);
+  a.gemm2_weights_scale = fake(0x8002);
+  CHECK(moe_fp8_run_static(&a, NULL) == (T > MOE_FP8_STATIC_MAX_TOKENS ? MOE_FP8_ESTATIC_TOKENS : MOE_FP8_EALIGN));
+  valid_args(&a, T);
+  a.output = fake(0x9004);
+  CHECK(moe_fp8_run(&a, ws, ws_bytes, NULL) == MOE_FP8_EALIGN);
+  valid_args(&a, T);
+  CHECK(moe_fp8_run(&a, fake(0x10080), L.total_bytes, NULL) == MOE_FP8_EALIGN);
+  CHECK(moe_fp8_run_packed(&a, fake(0xa008), moe_fp8_packed_weights_bytes(), ws, ws_bytes, NULL) == MOE_FP8_EALIGN);
   /* workspace: missing or one byte short */
   valid_args(&a, T);
   CHECK(moe_fp8_run(&a, NULL, L.total_bytes, NULL) == MOE_FP8_EWORKSPACE);
@@ -175,6 +189,9 @@ int main(void) {
         MOE_FP8_EINVAL_POINTER);
   CHECK(moe_fp8_quantize_hidden(fake(0x1000), MOE_FP8_HIDDEN_BF16, -3, fake(0x2000), fake(0x3000), NULL) ==
         MOE_FP8_EINVAL_TOKENS);
+  CHECK(moe_fp8_quantize_hidden(fake(0x1004), MOE_FP8_HIDDEN_BF16, 16, fake(0x2000), fake(0x3000), NULL) ==
+        MOE_FP8_EALIGN);
+  CHECK(moe_fp8_workspace_init(fake(0x1040), 4096, NULL) == MOE_FP8_EALIGN);
 
   /* the workspace clear: null or too small for the control block */
   CHECK(moe_fp8_workspace_init(NULL, 4096, NULL) == MOE_FP8_EWORKSPACE);

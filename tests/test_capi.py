@@ -30,7 +30,7 @@ def test_constants_match_header(pkg):
     assert int(vals["MOE_FP8_HIDDEN"]) == L.HIDDEN and int(vals["MOE_FP8_INTER"]) == L.INTER
     assert int(vals["MOE_FP8_EXPERTS_LOCAL"]) == L.EXPERTS_LOCAL
     for name in ("OK", "EINVAL_POINTER", "EINVAL_TOKENS", "EWORKSPACE", "EINVAL_BIAS_DTYPE",
-                 "EINVAL_OUT_DTYPE", "ELAUNCH", "EDEVICE", "EINVAL_HIDDEN_DTYPE", "ESTATIC_TOKENS", "EPACKED",
+                 "EINVAL_OUT_DTYPE", "ELAUNCH", "EDEVICE", "EINVAL_HIDDEN_DTYPE", "ESTATIC_TOKENS", "EPACKED", "EALIGN",
                  "STATIC_MAX_TOKENS", "PACKED_MAX_TOKENS"):
         assert int(vals["MOE_FP8_" + name]) == getattr(L, name)
     for name in ("HIDDEN_F32", "HIDDEN_BF16", "HIDDEN_F16", "BIAS_F32", "BIAS_BF16", "BIAS_F16"):
@@ -111,8 +111,11 @@ def test_argument_errors_are_reported_before_any_launch(pkg, lib):
     a = _args(pkg)
     a.routing_logits = None
     assert lib.moe_fp8_run(ctypes.byref(a), 0x1000, big, None) == L.EINVAL_POINTER
-    # ...but dispatch of given top-k lists does not need the router inputs
-    assert lib.moe_fp8_route_dispatch(ctypes.byref(a), 1, 0x1000, big, None) != L.EINVAL_POINTER
+    # ...but dispatch of given top-k lists does not need the router inputs (with a GPU present
+    # these placeholder addresses would pass every check and be launched on: not tried there)
+    import torch
+    if not torch.cuda.is_available():
+        assert lib.moe_fp8_route_dispatch(ctypes.byref(a), 1, 0x1000, big, None) == L.EDEVICE
     a = _args(pkg)
     a.num_tokens = -1
     assert lib.moe_fp8_run(ctypes.byref(a), 0x1000, big, None) == L.EINVAL_TOKENS
@@ -170,6 +173,56 @@ def test_no_device_is_reported(pkg, lib):
     L = pkg._lib
     a = _args(pkg)
     assert lib.moe_fp8_run(ctypes.byref(a), 0x1000, L.workspace_bytes(4), None) == L.EDEVICE
+
+
+@pytest.mark.parametrize("field,offset", [
+    ("routing_logits", 8), ("routing_bias", 2), ("hidden_states", 8), ("hidden_states_scale", 2),
+    ("gemm1_weights", 8), ("gemm1_weights_scale", 2), ("gemm2_weights", 8), ("gemm2_weights_scale", 2),
+    ("output", 4)])
+def test_misaligned_pointers_are_reported(pkg, lib, field, offset):
+    """A pointer off the alignment of the kernels' widest access to it is MOE_FP8_EALIGN, before
+    anything is launched. Calls whose placeholder addresses would pass every check are made only
+    without a GPU (they then stop at EDEVICE)."""
+    import torch
+    L = pkg._lib
+    big = L.workspace_bytes(4)
+    a = _args(pkg)
+    setattr(a, field, 0x1000 + offset)
+    assert lib.moe_fp8_run(ctypes.byref(a), 0x1000, big, None) == L.EALIGN
+    assert lib.moe_fp8_run_static(ctypes.byref(a), None) == L.EALIGN
+    if field not in ("routing_logits", "routing_bias"):
+        assert lib.moe_fp8_gemm1(ctypes.byref(a), 0x1000, big, None) == L.EALIGN
+    elif not torch.cuda.is_available():
+        # the GEMM stages do not read the router inputs and do not check them
+        assert lib.moe_fp8_gemm1(ctypes.byref(a), 0x1000, big, None) == L.EDEVICE
+    if not torch.cuda.is_available():
+        # bf16 bias (2 bytes) and bf16 output (8) accept what fp32 would not
+        a = _args(pkg)
+        a.routing_bias = 0x1002
+        a.routing_bias_dtype = L.BIAS_BF16
+        a.output = 0x1008
+        a.output_dtype = L.OUT_BF16
+        assert lib.moe_fp8_run(ctypes.byref(a), 0x1000, big, None) == L.EDEVICE
+        a.routing_bias_dtype = L.BIAS_F32
+        assert lib.moe_fp8_run(ctypes.byref(a), 0x1000, big, None) == L.EALIGN
+
+
+def test_misaligned_workspace_and_buffers_are_reported(pkg, lib):
+    L = pkg._lib
+    big = L.workspace_bytes(4)
+    a = _args(pkg)
+    assert lib.moe_fp8_run(ctypes.byref(a), 0x1080, big, None) == L.EALIGN
+    assert lib.moe_fp8_workspace_init(0x1080, big, None) == L.EALIGN
+    n = L.packed_weights_bytes()
+    assert lib.moe_fp8_run_packed(ctypes.byref(a), 0x1008, n, 0x1000, big, None) == L.EALIGN
+    assert lib.moe_fp8_pack_weights(ctypes.byref(a), 0x1008, n, None) == L.EALIGN
+    a.gemm2_weights = 0x2004
+    assert lib.moe_fp8_pack_weights(ctypes.byref(a), 0x1000, n, None) == L.EALIGN
+    f = lib.moe_fp8_quantize_hidden
+    assert f(0x1008, L.HIDDEN_BF16, 4, 0x2000, 0x3000, None) == L.EALIGN
+    assert f(0x1000, L.HIDDEN_BF16, 4, 0x2004, 0x3000, None) == L.EALIGN
+    assert f(0x1000, L.HIDDEN_BF16, 4, 0x2000, 0x3002, None) == L.EALIGN
+    assert "aligned" in L.strerror(L.EALIGN)
 
 
 def test_quantize_hidden_argument_errors(pkg, lib):

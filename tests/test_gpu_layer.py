@@ -425,6 +425,38 @@ def test_strided_inputs_give_the_same_output(name):
     assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
 
 
+def _offset_copy(t, nbytes):
+    """A contiguous copy of t whose data starts nbytes past an allocation's (aligned) start."""
+    buf = torch.zeros(nbytes + t.numel() * t.element_size(), dtype=torch.uint8, device=t.device)
+    v = buf[nbytes:].view(t.dtype).view(t.shape)
+    v.copy_(t)
+    return v
+
+
+@pytest.mark.parametrize("name", ["t16", "t1024_off64"])
+def test_misaligned_inputs_give_the_same_output(name):
+    """Tensors whose data is off the alignment of the kernels' vector accesses (logits 4 bytes
+    off, hidden states and W2 8 bytes off, the bf16 output 2 bytes off) are accepted as the
+    reference accepts them: run() copies such inputs and writes such an output through a
+    temporary, and the result is the aligned call's bit for bit (the C ABI itself reports such
+    pointers as MOE_FP8_EALIGN)."""
+    gh = _gh()
+    kw, _ = _workload(name)
+    ref = _run_full(kw)
+    kw2 = dict(kw, routing_logits=_offset_copy(kw["routing_logits"], 4),
+               hidden_states=_offset_copy(kw["hidden_states"], 8),
+               gemm2_weights=_offset_copy(kw["gemm2_weights"], 8))
+    for k, n in (("routing_logits", 16), ("hidden_states", 16), ("gemm2_weights", 16)):
+        assert kw2[k].data_ptr() % n != 0 and kw2[k].is_contiguous()
+    out = _offset_copy(torch.full_like(ref, float("nan")), 2)
+    assert out.data_ptr() % 8 != 0
+    gh.pkg.run(**kw2, output=out)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+    del kw2
+    torch.cuda.empty_cache()
+
+
 def _given_topk(case, T, rng):
     ids = np.stack([rng.permutation(256)[:8] for _ in range(T)]).astype(np.int32)
     if case == "one_expert":                     # every token on local expert 5, nothing else local

@@ -90,6 +90,24 @@ def test_layer_on_quantized_input():
     assert torch.equal(out_a, out_b)
 
 
+def test_misaligned_buffers():
+    """Input and output buffers off the kernel's access alignment (bf16 input 4 bytes off, fp8
+    output 4 bytes off) give the aligned call's codes and scales."""
+    gh = _gh()
+    x = _hidden(37, 11).to(torch.bfloat16).to("cuda")
+    q_ref, s_ref = gh.pkg.quantize_hidden(x)
+    xb = torch.zeros(4 + x.numel() * 2, dtype=torch.uint8, device="cuda")
+    xm = xb[4:].view(torch.bfloat16).view(x.shape)
+    xm.copy_(x)
+    ob = torch.zeros(4 + q_ref.numel(), dtype=torch.uint8, device="cuda")
+    qm = ob[4:].view(torch.float8_e4m3fn).view(q_ref.shape)
+    assert xm.data_ptr() % 16 != 0 and qm.data_ptr() % 8 != 0
+    q, s = gh.pkg.quantize_hidden(xm, out=qm)
+    torch.cuda.synchronize()
+    assert q.data_ptr() == qm.data_ptr()
+    assert torch.equal(q.view(torch.uint8), q_ref.view(torch.uint8)) and torch.equal(s, s_ref)
+
+
 def test_validation():
     gh = _gh()
     with pytest.raises(AssertionError, match="hidden must be \\[T, 7168\\]"):
