@@ -84,6 +84,10 @@ class Workspace:
         self.nbytes = int(self.layout.total_bytes)
         self.buffer = torch.empty(max(self.nbytes, 256), dtype=torch.uint8, device=device)
         self.captured = False   # set once a graph capture has recorded a call using it
+        # held while a call queues its kernels: calls from several host threads on one stream
+        # (ctypes releases the GIL) then queue whole launch sequences one after another, so that
+        # the kernels of two calls never interleave on the stream they share with the workspace
+        self.lock = threading.Lock()
         stream = stream or torch.cuda.current_stream(device)
         _lib.check(_lib.load().moe_fp8_workspace_init(self.buffer.data_ptr(), self.buffer.numel(),
                                                       stream.cuda_stream), "moe_fp8_workspace_init")
@@ -411,13 +415,14 @@ def _run(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1
         if packed is _AUTO:
             packed = _packed_weights.get(w13, w2) if (
                 T <= PACKED_MAX_TOKENS and w13 is gemm1_weights and w2 is gemm2_weights) else None
-        if packed is None:
-            _lib.check(lib.moe_fp8_run(args, ws.ptr, ws.buffer.numel(), stream), "moe_fp8_run")
-        else:
-            if packed.device != dev:
-                raise RuntimeError(f"packed_weights must be on {dev}; got {packed.device}")
-            _lib.check(lib.moe_fp8_run_packed(args, packed.data_ptr(), packed.numel(), ws.ptr, ws.buffer.numel(),
-                                              stream), "moe_fp8_run_packed")
+        if packed is not None and packed.device != dev:
+            raise RuntimeError(f"packed_weights must be on {dev}; got {packed.device}")
+        with ws.lock:
+            if packed is None:
+                _lib.check(lib.moe_fp8_run(args, ws.ptr, ws.buffer.numel(), stream), "moe_fp8_run")
+            else:
+                _lib.check(lib.moe_fp8_run_packed(args, packed.data_ptr(), packed.numel(), ws.ptr,
+                                                  ws.buffer.numel(), stream), "moe_fp8_run_packed")
     if not direct:
         output.copy_(dst)
 

@@ -391,6 +391,44 @@ def test_two_streams_at_once():
             assert torch.equal(o.view(torch.int16), ref.view(torch.int16)), f"stream {n} call {i} differs"
 
 
+def test_two_threads_on_one_stream():
+    """run() from two host threads at once on one stream (each thread's current stream is the
+    device's default stream, so they share its workspace; ctypes releases the GIL during the
+    C call): each call queues its whole launch sequence under the workspace's lock, and every
+    output equals the call alone, bit for bit."""
+    import threading
+    gh = _gh()
+    dev = torch.device("cuda:0")
+    kw = {"a": _workload("t64")[0], "b": _workload("t1024_off64")[0]}
+    ref = {n: _run_full(k) for n, k in kw.items()}
+    print("two threads on one stream: t64 and t1024_off64, 6 calls each", flush=True)
+    outs, errors = {}, []
+
+    def worker(n):
+        try:
+            torch.cuda.set_device(dev)
+            res = []
+            for _ in range(6):
+                o = torch.full_like(ref[n], float("nan"))
+                gh.pkg.run(**kw[n], output=o)
+                res.append(o)
+            outs[n] = res
+        except Exception as e:   # reported below, in the test's own thread
+            errors.append(repr(e))
+
+    threads = [threading.Thread(target=worker, args=(n,)) for n in kw]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=120)
+    assert not any(t.is_alive() for t in threads), "a worker thread did not finish"
+    assert not errors, errors
+    torch.cuda.synchronize()
+    for n in kw:
+        for i, o in enumerate(outs[n]):
+            assert torch.equal(o.view(torch.int16), ref[n].view(torch.int16)), f"thread {n} call {i} differs"
+
+
 def test_cpu_output_and_inputs_are_moved():
     gh = _gh()
     kw, _ = _workload("t16")
