@@ -1060,8 +1060,11 @@ hipError_t launch_gemm2(const GemmParams& p, int rows_per_item, bool packed, hip
 
 hipError_t launch_combine(const GemmParams& p, int rows_per_item, hipStream_t s) {
   if (p.T <= 0 || rows_per_item == kFusedItemRows) return hipSuccess;   // combined in GEMM2
-  int grid = (p.T * kCombineChunks + 3) / 4;   // 4 (token, chunk) items per work-group at a time
-  if (grid > num_cus() * 8) grid = num_cus() * 8;
+  // 4 (token, chunk) items per work-group at a time; up to 32 work-groups per CU (against 8:
+  // GEMM2 + combine at T=8192 247-248 -> 243-244 us, unchanged at T=1024 and on the skewed
+  // T=4096 batch)
+  int grid = (p.T * kCombineChunks + 3) / 4;
+  if (grid > num_cus() * 32) grid = num_cus() * 32;
   hipLaunchKernelGGL(combine_kernel, dim3(grid), dim3(256), 0, s, p);
   return hipGetLastError();
 }
