@@ -16,15 +16,15 @@ inline size_t align_up(size_t x) { return (x + kAlign - 1) & ~(kAlign - 1); }
 
 int check_device() {
   // per device: 0 unknown, 1 gfx950, -1 another GPU (concurrent first calls store the same)
-  static std::atomic<int> verdict[64] = {};
+  static std::atomic<int> arch_ok[64] = {};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0) return MOE_FP8_EDEVICE;
-  int v = dev < 64 ? verdict[dev].load(std::memory_order_relaxed) : 0;
+  int v = dev < 64 ? arch_ok[dev].load(std::memory_order_relaxed) : 0;
   if (v == 0) {
     hipDeviceProp_t prop;
     if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return MOE_FP8_EDEVICE;
     v = strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 1 : -1;
-    if (dev < 64) verdict[dev].store(v, std::memory_order_relaxed);   // devices past 64: uncached
+    if (dev < 64) arch_ok[dev].store(v, std::memory_order_relaxed);   // devices past 64: uncached
   }
   return v == 1 ? MOE_FP8_OK : MOE_FP8_EDEVICE;
 }
