@@ -579,6 +579,57 @@ def test_layer_edge_cases_given_topk(T, case):
         assert np.all(got[640:] == 0)
 
 
+@pytest.mark.parametrize("T,density,seed", [(7, 1.0, 1), (150, 0.3, 2), (300, 1.0, 3), (777, 0.1, 4), (1500, 0.7, 5),
+                                            (2900, 0.02, 6), (4099, 0.3, 7), (6000, 1.0, 8)])
+def test_random_topk_lists(T, density, seed):
+    """The GEMM stages on random given top-k lists: every slot local with probability `density`
+    (then a uniform local expert, so a token may name one expert several times), otherwise any
+    of the 256 experts; random weights. The dispatch bit-exact, the intermediate and GEMM2 +
+    combine within the per-element bounds, the output within the emulated oracle's relative
+    RMS, and tokens without a local slot exactly zero."""
+    gh = _gh()
+    dev = torch.device("cuda:0")
+    w, wnp = _weights()
+    print(f"random top-k lists T={T} density={density}", flush=True)
+    rng = np.random.default_rng(seed)
+    ids = rng.integers(0, 256, (T, 8)).astype(np.int32)
+    loc = rng.random((T, 8)) < density
+    ids[loc] = rng.integers(0, 32, int(loc.sum()))
+    tw = (rng.random((T, 8)) * 0.5).astype(np.float32)
+    logits, bias, hq, hs = gh.inputs.make_activations(T, 700 + seed, dev)
+    kw = dict(routing_logits=logits, routing_bias=bias, hidden_states=hq, hidden_states_scale=hs,
+              gemm1_weights=w[0], gemm1_weights_scale=w[1], gemm2_weights=w[2], gemm2_weights_scale=w[3],
+              local_expert_offset=0, routed_scaling_factor=2.5)
+    out = torch.full((T, 7168), float("nan"), dtype=torch.bfloat16, device=dev)
+    ws = gh.new_workspace(T, dev)
+    gh.write(ws, "topk_ids", ids)
+    gh.write(ws, "topk_weights", tw)
+    args = gh.make_args(**kw, output=out)
+    gh.route_dispatch(args, ws, skip_routing=1)
+    gh.check_dispatch(ws, ids, tw, 0, T)
+    gh.gemm1(args, ws)
+    gh.gemm2_combine(args, ws)
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    assert np.isfinite(got).all()
+    npkw = gh.to_numpy_inputs({**kw, "gemm1_weights": w[0][:1], "gemm2_weights": w[2][:1]})
+    npkw["gemm1_weights"], npkw["gemm1_weights_scale"], npkw["gemm2_weights"], npkw["gemm2_weights_scale"] = wnp
+    npkw["dequant_cache"] = _WEIGHTS["cache"]
+    tokens = None if T <= 40 else np.sort(rng.choice(T, 16, replace=False))
+    emu = olayer.layer_forward(**npkw, mode="emulated", topk=(ids, tw), tokens=tokens, requant_block=_requant_block(T))
+    sel = slice(None) if tokens is None else tokens
+    what = f"random top-k T={T} density={density}"
+    n = len(emu["sorted_slot"])
+    act, sc = _read_act(ws, n)
+    _check_intermediate(act, sc, emu, _wanted_rows(emu, tokens), what)
+    _check_second_half(got[sel], npkw, act, sc, tokens, what, topk=(ids, tw))
+    g, r = got[sel], emu["output"]
+    rel = np.sqrt(np.mean((g - r) ** 2)) / max(np.sqrt(np.mean(r ** 2)), 1e-30)
+    print(f"{what} vs emulated oracle: rel rms {rel:.4g}", flush=True)
+    assert rel <= 0.01
+    assert np.all(got[np.sum(ids < 32, axis=1) == 0] == 0)
+
+
 @pytest.mark.parametrize("T,offset", [(2, 208), (3, 0), (33, 160), (65, 32), (129, 224), (257, 96), (511, 0),
                                       (1000, 64), (2047, 128), (4097, 192), (9001, 0)])
 def test_odd_batches_match_oracle(T, offset):
