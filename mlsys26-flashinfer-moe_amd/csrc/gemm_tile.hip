@@ -78,10 +78,12 @@ constexpr int kWDma = kTileW / kTileWaves / 8;       // weight DMA loads per wav
 //             (capped at the last one) for waves 4-7.
 // Columns per requantisation scale of GEMM1's output (kQCols): the reference's 64
 // (kernel.py:131-135) with 128-row items, so that GEMM2 applies two activation scales per
-// 128-wide K-step (one MFMA per 64-column half, the other half's bytes zeroed); 128 with
-// 160-row items (T >= 4096), one scale and one MFMA per fragment. Measured with 64 there
-// too: GEMM2 + combine 249 -> 323 us at T=8192 and 552 -> 732 us on the skewed T=4096 batch
-// (its MFMAs double), against 115 -> 121 us at T=1024.
+// 128-wide K-step: it runs v_mfma_f32_32x32x64_f8f6f4 on 32-row item groups, one MFMA per
+// 64-column half (against two 16x16x128 MFMAs per fragment with the other half's bytes
+// zeroed: the same time at T=1024, half the matrix-core work); 128 with 160-row items
+// (T >= 4096), one scale and one 16x16x128 MFMA per fragment. Measured with 64 there too, in
+// the zeroed-half form: GEMM2 + combine 249 -> 323 us at T=8192 and 552 -> 732 us on the
+// skewed T=4096 batch (its MFMAs double), against 115 -> 121 us at T=1024.
 template <int ROWS>
 struct TileShape {
   static constexpr int kRows = ROWS;
@@ -93,6 +95,10 @@ struct TileShape {
   static constexpr int kQBlocks = kInter / kQCols;        // activation scales per row
   static constexpr int kSHalves = kBlock / kQCols;        // GEMM2 activation scales per K-step
   static constexpr int kMaxNG = (ROWS / 16 + 1) / 2;      // row groups of a wavefront half
+  // GEMM2 with two activation scales per K-step: v_mfma_f32_32x32x64_f8f6f4, one MFMA per
+  // 64-wide half of the K-step, on 32-row item groups (kW32)
+  static constexpr bool kW32 = kSHalves == 2;
+  static constexpr int kMaxNG32 = (ROWS / 32 + 1) / 2;    // 32-row groups of a wavefront half
   static constexpr int kLoadsPerStep = kWDma + 3;
   static_assert(ROWS % 16 == 0 && (kABlocks == 2 * kTileWaves || kABlocks == 2 * kTileWaves + 4), "tile rows");
   static_assert(kSBlocks <= 4, "scale blocks");
@@ -160,6 +166,13 @@ __device__ __forceinline__ v8i lds_frag(const uint8_t* buf, int m, int lane) {
               *reinterpret_cast<const v4i*>(buf + swz(m, 4 + (lane >> 4))));
 }
 
+// A 32-row operand of one 64-wide half hh of a K-step (rows m0 .. m0+31 of an LDS tile, for
+// v_mfma_f32_32x32x64_f8f6f4): lane l holds row m0 + l%32, chunks 4hh + 2(l/32) and the next.
+__device__ __forceinline__ v8i lds_frag32(const uint8_t* buf, int m, int hh, int lane) {
+  const int c = 4 * hh + 2 * (lane >> 5);
+  return join(*reinterpret_cast<const v4i*>(buf + swz(m, c)), *reinterpret_cast<const v4i*>(buf + swz(m, c + 1)));
+}
+
 // One unit (c). Its K-steps read ring stages s_base, s_base+1, .. (mod 3). GEMM2 (16 K-steps
 // per unit) prefetches across units: its last two steps load the first two steps of the next
 // unit (n) when `have_n`, and `pre` says that this unit's were loaded so. GEMM1 (56 K-steps)
@@ -171,8 +184,9 @@ __device__ __forceinline__ void tile_body(const GemmParams& p, const TileCtx<ROW
                                           int32_t* queue) {
   using S = TileShape<ROWS>;
   constexpr int KS = G1 ? kHBlocks : kIBlocks;
-  // GEMM2 with two activation scales per K-step (64-column requantisation blocks)
-  constexpr bool H2 = !G1 && S::kSHalves == 2;
+  // GEMM2 with two activation scales per K-step (64-column requantisation blocks): 32x32x64
+  // MFMAs, NG counts 32-row item groups
+  constexpr bool W32 = !G1 && S::kW32;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wb = wave & 3;     // weight rows 64*wb.. (item rows: the wave's half, from c.m0)
@@ -206,12 +220,22 @@ __device__ __forceinline__ void tile_body(const GemmParams& p, const TileCtx<ROW
     }
   };
 
-  v4f acc[4][NG > 0 ? NG : 1];
-#pragma unroll
-  for (int f = 0; f < 4; ++f)
-#pragma unroll
-    for (int g = 0; g < NG; ++g) acc[f][g] = v4f{0.f, 0.f, 0.f, 0.f};
+  constexpr int NG1 = NG > 0 ? NG : 1;
+  v4f acc[W32 ? 1 : 4][W32 ? 1 : NG1];
+  v16f acc32[W32 ? 2 : 1][W32 ? NG1 : 1];   // W32: [weight rows 32*blk..][item group]
   const v4f zero = {0.f, 0.f, 0.f, 0.f};
+  const v16f zero16 = {};
+  if constexpr (W32) {
+#pragma unroll
+    for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+      for (int g = 0; g < NG; ++g) acc32[blk][g] = zero16;
+  } else {
+#pragma unroll
+    for (int f = 0; f < 4; ++f)
+#pragma unroll
+      for (int g = 0; g < NG; ++g) acc[f][g] = zero;
+  }
 
   // weight fragment f of this wave: GEMM1 gate rows 32*wb + 16f (f = 0,1) and the up rows
   // 128 + 32*wb + 16(f-2) (f = 2,3); GEMM2 rows 64*wb + 16f
@@ -227,16 +251,35 @@ __device__ __forceinline__ void tile_body(const GemmParams& p, const TileCtx<ROW
     v8i wf[4];
     v8i bf;
     float sa;
-    float sa2;   // H2: the scale of the K-step's second 64-column half
   };
   auto load_head = [&](int s, Head& h) {
     if constexpr (NG > 0) {
       const TileStage<ROWS>& st = sh.st[s];
       h.bf = lds_frag(st.a + c.m0 * 128, lane & 15, lane);
       h.sa = st.sa[c.m0 + (lane & 15)];
-      h.sa2 = H2 ? st.sa[S::kSSlots + c.m0 + (lane & 15)] : 0.f;
 #pragma unroll
       for (int f = 0; f < 4; ++f) h.wf[f] = lds_frag(st.w, wrow(f), lane);
+    }
+  };
+  // W32: the wave's two 32-row weight blocks and its first item group, each as two 64-wide
+  // halves, and that group's two activation scales
+  struct Head32 {
+    v8i wf[2][2];
+    v8i bf[2];
+    float sa[2];
+  };
+  auto load_head32 = [&](int s, Head32& h) {
+    if constexpr (NG > 0) {
+      const TileStage<ROWS>& st = sh.st[s];
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        h.bf[hh] = lds_frag32(st.a, c.m0 + (lane & 31), hh, lane);
+        h.sa[hh] = st.sa[S::kSSlots * hh + c.m0 + (lane & 31)];
+      }
+#pragma unroll
+      for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) h.wf[blk][hh] = lds_frag32(st.w, 64 * wb + 32 * blk + (lane & 31), hh, lane);
     }
   };
 
@@ -245,8 +288,7 @@ __device__ __forceinline__ void tile_body(const GemmParams& p, const TileCtx<ROW
   // the first group of the next step runs), so that the matrix core is not idle during the
   // VALU work. dp holds the pending group's MFMA results, p0/p1 its two scale products.
   v4f dp[4] = {zero, zero, zero, zero};
-  v4f dp2[4] = {zero, zero, zero, zero};   // H2: the second half's pending results
-  float p0 = 0.f, p1 = 0.f, p2 = 0.f;
+  float p0 = 0.f, p1 = 0.f;
 
   auto compute = [&](int s, const Head& h, float s0, float s1) __attribute__((always_inline)) {
     if constexpr (NG > 0) {
@@ -254,55 +296,73 @@ __device__ __forceinline__ void tile_body(const GemmParams& p, const TileCtx<ROW
       const v8i (&wf)[4] = h.wf;
       v8i bf = h.bf;
       float sa = h.sa;
-      float sa2 = h.sa2;
 #pragma unroll
       for (int g = 0; g < NG; ++g) {
         // the next row group's fragment is read from LDS while this group's MFMAs run
         v8i bf_next = bf;
         float sa_next = sa;
-        float sa2_next = sa2;
         if (g + 1 < NG) {
           bf_next = lds_frag(st.a + c.m0 * 128, 16 * (g + 1) + (lane & 15), lane);
           sa_next = st.sa[c.m0 + 16 * (g + 1) + (lane & 15)];
-          if constexpr (H2) sa2_next = st.sa[S::kSSlots + c.m0 + 16 * (g + 1) + (lane & 15)];
         }
         // pending group: the previous group of this step, or the previous step's last
         // group (zero results and zero scales before the first step)
         const int gp = g == 0 ? NG - 1 : g - 1;
-        v4f d[4], d2[4];
-        if constexpr (H2) {
-          // one MFMA per 64-column half of the activation fragment (lanes hold bytes
-          // [16j, 16j+16) of the first half in bf[0..3] and of the second in bf[4..7])
-          const v4i kZero4 = {0, 0, 0, 0};
-          const v8i b_lo = join(lo_half(bf), kZero4);
-          const v8i b_hi = join(kZero4, hi_half(bf));
+        v4f d[4];
 #pragma unroll
-          for (int f = 0; f < 4; ++f) {
-            d[f] = mfma16x16x128_fp8(wf[f], b_lo, zero);
-            d2[f] = mfma16x16x128_fp8(wf[f], b_hi, zero);
-            acc[f][gp] += dp[f] * p0;
-            acc[f][gp] += dp2[f] * p2;
-          }
-#pragma unroll
-          for (int f = 0; f < 4; ++f) dp2[f] = d2[f];
-        } else {
-#pragma unroll
-          for (int f = 0; f < 4; ++f) {
-            d[f] = mfma16x16x128_fp8(wf[f], bf, zero);
-            acc[f][gp] += dp[f] * (f < 2 ? p0 : p1);
-          }
+        for (int f = 0; f < 4; ++f) {
+          d[f] = mfma16x16x128_fp8(wf[f], bf, zero);
+          acc[f][gp] += dp[f] * (f < 2 ? p0 : p1);
         }
 #pragma unroll
         for (int f = 0; f < 4; ++f) dp[f] = d[f];
         p0 = sa * s0;
         p1 = sa * s1;
-        if constexpr (H2) p2 = sa2 * s0;
         // two row groups' MFMA results live at a time (the scheduler would otherwise hoist
         // every MFMA of the step and hold all their results)
         __builtin_amdgcn_sched_barrier(0);
         bf = bf_next;
         sa = sa_next;
-        sa2 = sa2_next;
+      }
+    }
+  };
+
+  // W32: per item group the four MFMAs (two weight blocks x two K halves) first, then their
+  // scale promotion, acc += d_h * (s_act,h * s_w), in issue order, so that each FMA finds its
+  // MFMA done; the next group's fragment and scales are read from LDS meanwhile.
+  auto compute32 = [&](int s, const Head32& h, float s0) __attribute__((always_inline)) {
+    if constexpr (NG > 0) {
+      const TileStage<ROWS>& st = sh.st[s];
+      v8i bf[2] = {h.bf[0], h.bf[1]};
+      float sa[2] = {h.sa[0], h.sa[1]};
+#pragma unroll
+      for (int g = 0; g < NG; ++g) {
+        v8i bf_next[2] = {bf[0], bf[1]};
+        float sa_next[2] = {sa[0], sa[1]};
+        if (g + 1 < NG) {
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh) {
+            bf_next[hh] = lds_frag32(st.a, c.m0 + 32 * (g + 1) + (lane & 31), hh, lane);
+            sa_next[hh] = st.sa[S::kSSlots * hh + c.m0 + 32 * (g + 1) + (lane & 31)];
+          }
+        }
+        v16f d[2][2];
+#pragma unroll
+        for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh) d[blk][hh] = mfma32x32x64_fp8(h.wf[blk][hh], bf[hh], zero16);
+        const float q0 = sa[0] * s0, q1 = sa[1] * s0;
+#pragma unroll
+        for (int blk = 0; blk < 2; ++blk) {
+          acc32[blk][g] += d[blk][0] * q0;
+          acc32[blk][g] += d[blk][1] * q1;
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          bf[hh] = bf_next[hh];
+          sa[hh] = sa_next[hh];
+        }
       }
     }
   };
@@ -325,24 +385,30 @@ __device__ __forceinline__ void tile_body(const GemmParams& p, const TileCtx<ROW
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __builtin_amdgcn_s_barrier();
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    Head h;
-    load_head(s_cur, h);
-    __builtin_amdgcn_sched_barrier(0);
-    issue(k + 2, s_next);
-    __builtin_amdgcn_sched_barrier(0);
     const float s0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sw0_lane), k));
-    const float s1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sw1_lane), k));
-    compute(s_cur, h, s0, s1);
+    if constexpr (W32) {
+      Head32 h;
+      load_head32(s_cur, h);
+      __builtin_amdgcn_sched_barrier(0);
+      issue(k + 2, s_next);
+      __builtin_amdgcn_sched_barrier(0);
+      compute32(s_cur, h, s0);
+    } else {
+      Head h;
+      load_head(s_cur, h);
+      __builtin_amdgcn_sched_barrier(0);
+      issue(k + 2, s_next);
+      __builtin_amdgcn_sched_barrier(0);
+      const float s1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sw1_lane), k));
+      compute(s_cur, h, s0, s1);
+    }
     s_cur = s_cur == kStages - 1 ? 0 : s_cur + 1;
     s_next = s_next == kStages - 1 ? 0 : s_next + 1;
   }
   // the last step's last row group
-  if constexpr (NG > 0) {
+  if constexpr (NG > 0 && !W32) {
 #pragma unroll
-    for (int f = 0; f < 4; ++f) {
-      acc[f][NG - 1] += dp[f] * (f < 2 ? p0 : p1);
-      if constexpr (H2) acc[f][NG - 1] += dp2[f] * p2;
-    }
+    for (int f = 0; f < 4; ++f) acc[f][NG - 1] += dp[f] * (f < 2 ? p0 : p1);
   }
   // The loads in flight now are the next unit's first two steps, or reloads nobody reads; the
   // reloads must land before the next unit refills the ring.
@@ -406,36 +472,50 @@ __device__ __forceinline__ void tile_body(const GemmParams& p, const TileCtx<ROW
     // next unit's prefetched K-steps: vmcnt counts in order; deriving the destination here from
     // the token's local count took a second, dependent round trip). Rows past the item read its
     // first row.
+    // (W32: the lane's row is c.m0 + 32g + lane%32, its 16 values four runs of 4 consecutive
+    // hidden columns, 8q + 4(lane/32) .. +3 of each 32-row weight block)
+    constexpr int kGRows = W32 ? 32 : 16;
     int dest[NG > 0 ? NG : 1];
     float wt[NG > 0 ? NG : 1];
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
-      const int m = c.m0 + 16 * g + (lane & 15);
+      const int m = c.m0 + kGRows * g + (lane & (kGRows - 1));
       const int pr = c.r0 + (m < c.rows ? m : 0);
       dest[g] = p.row_dest[pr];
       wt[g] = p.sorted_weight[pr];
     }
     if (queue != nullptr && threadIdx.x == 0) sh.next = got;
+    auto store4 = [&](bool direct, int t, size_t slot, int h, const v4f& val) __attribute__((always_inline)) {
+      if (direct) {
+        if (p.out_dtype == MOE_FP8_OUT_BF16)
+          *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(p.out) + (size_t)t * kHidden + h) =
+              pack_bf16x4(val[0], val[1], val[2], val[3]);
+        else
+          *reinterpret_cast<v4f*>(reinterpret_cast<float*>(p.out) + (size_t)t * kHidden + h) = val;
+      } else {
+        *reinterpret_cast<v4f*>(p.partial + slot * kHidden + h) = val;
+      }
+    };
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
-      const int m = c.m0 + 16 * g + (lane & 15);
+      const int m = c.m0 + kGRows * g + (lane & (kGRows - 1));
       if (m < c.rows) {
         const bool direct = dest[g] >= 0;
         const int t = dest[g];
         const size_t slot = (size_t)(-1 - dest[g]);
+        if constexpr (W32) {
 #pragma unroll
-        for (int f = 0; f < 4; ++f) {
-          const v4f val = acc[f][g] * wt[g];
-          const int h = c.tile * kTileW + 64 * wb + 16 * f + 4 * (lane >> 4);
-          if (direct) {
-            if (p.out_dtype == MOE_FP8_OUT_BF16)
-              *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(p.out) + (size_t)t * kHidden + h) =
-                  pack_bf16x4(val[0], val[1], val[2], val[3]);
-            else
-              *reinterpret_cast<v4f*>(reinterpret_cast<float*>(p.out) + (size_t)t * kHidden + h) = val;
-          } else {
-            *reinterpret_cast<v4f*>(p.partial + slot * kHidden + h) = val;
-          }
+          for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const v16f& a = acc32[blk][g];
+              const v4f val = v4f{a[4 * q], a[4 * q + 1], a[4 * q + 2], a[4 * q + 3]} * wt[g];
+              store4(direct, t, slot, c.tile * kTileW + 64 * wb + 32 * blk + 8 * q + 4 * (lane >> 5), val);
+            }
+        } else {
+#pragma unroll
+          for (int f = 0; f < 4; ++f)
+            store4(direct, t, slot, c.tile * kTileW + 64 * wb + 16 * f + 4 * (lane >> 4), acc[f][g] * wt[g]);
         }
       }
     }
@@ -448,7 +528,8 @@ template <bool G1, int ROWS, int NG = 0>
 __device__ __forceinline__ void tile_body_ng(const GemmParams& p, const TileCtx<ROWS>& c, const TileCtx<ROWS>& n,
                                              bool have_n, int s_base, bool pre, TileShared<ROWS>& sh,
                                              int32_t* queue) {
-  if constexpr (NG < TileShape<ROWS>::kMaxNG) {
+  constexpr int kMax = (!G1 && TileShape<ROWS>::kW32) ? TileShape<ROWS>::kMaxNG32 : TileShape<ROWS>::kMaxNG;
+  if constexpr (NG < kMax) {
     if (c.ng == NG) tile_body<G1, NG, ROWS>(p, c, n, have_n, s_base, pre, sh, queue);
     else tile_body_ng<G1, ROWS, NG + 1>(p, c, n, have_n, s_base, pre, sh, queue);
   } else {
@@ -525,11 +606,13 @@ __device__ __forceinline__ void unit_setup(const GemmParams& p, int u, TileCtx<R
   }
   c.sw0_lane = swp0[lane < KS ? lane : 0];
   c.sw1_lane = swp1[lane < KS ? lane : 0];
-  // the item's row groups, split between the two wavefront halves (half 0 takes the odd one)
-  const int groups = (c.rows + 15) >> 4;
+  // the item's row groups (16 rows; 32 for the 32x32x64 GEMM2), split between the two
+  // wavefront halves (half 0 takes the odd one)
+  constexpr int kGRows = (!G1 && S::kW32) ? 32 : 16;
+  const int groups = (c.rows + kGRows - 1) / kGRows;
   const int g0 = (groups + 1) >> 1;
   c.ng = (wave >> 2) == 0 ? g0 : groups - g0;
-  c.m0 = (wave >> 2) == 0 ? 0 : 16 * g0;
+  c.m0 = (wave >> 2) == 0 ? 0 : kGRows * g0;
 }
 
 // A per-XCD work list (see the top of the file). Lane k < 32 of every wavefront holds

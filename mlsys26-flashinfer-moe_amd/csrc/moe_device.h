@@ -9,6 +9,7 @@ namespace moe {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v8i __attribute__((ext_vector_type(8)));
 typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
 
 // Logistic function sigma(x) = 1 / (1 + e^-x) as a fixed sequence of IEEE fp32
 // operations (no contraction), so that a host restatement with the same operations
@@ -65,6 +66,13 @@ __device__ __forceinline__ uint32_t pack_fp8x4(float a, float b, float c, float 
 // The result lane l holds D[4*(l/16)+i][l%16], i = 0..3.
 __device__ __forceinline__ v4f mfma16x16x128_fp8(const v8i& a, const v8i& b, const v4f& c) {
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+}
+
+// D[32x32] (+)= A[32x64] * B[64x32], fp8 e4m3 operands, fp32 accumulate.
+// Lane l supplies row (A) / column (B) l%32 and the 32 K-bytes [(l/32)*32, +32).
+// The result lane l holds D[8*(i/4) + 4*(l/32) + i%4][l%32], i = 0..15.
+__device__ __forceinline__ v16f mfma32x32x64_fp8(const v8i& a, const v8i& b, const v16f& c) {
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
 }
 
 __device__ __forceinline__ v8i join(const v4i& lo, const v4i& hi) {
