@@ -81,9 +81,11 @@ constexpr int kWDma = kTileW / kTileWaves / 8;       // weight DMA loads per wav
 // 128-wide K-step: it runs v_mfma_f32_32x32x64_f8f6f4 on 32-row item groups, one MFMA per
 // 64-column half (against two 16x16x128 MFMAs per fragment with the other half's bytes
 // zeroed: the same time at T=1024, half the matrix-core work); 128 with 160-row items
-// (T >= 4096), one scale and one 16x16x128 MFMA per fragment. Measured with 64 there too, in
-// the zeroed-half form: GEMM2 + combine 249 -> 323 us at T=8192 and 552 -> 732 us on the
-// skewed T=4096 batch (its MFMAs double), against 115 -> 121 us at T=1024.
+// (T >= 4096), one scale and one 16x16x128 MFMA per fragment. Measured with 64 there too:
+// GEMM2 + combine at T=8192 238-242 -> 274-283 us and on the skewed T=4096 batch 539-542 ->
+// 623-625 us with 32x32x64 MFMAs on 32-row groups (both halves' scales row-interleaved in LDS,
+// an eighth load per wavefront and K-step, 256 registers), 249 -> 323 and 552 -> 732 with
+// the zeroed-half 16x16x128 form: the doubled scale promotion costs what remains.
 template <int ROWS>
 struct TileShape {
   static constexpr int kRows = ROWS;
