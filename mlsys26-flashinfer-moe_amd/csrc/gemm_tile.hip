@@ -34,13 +34,15 @@
 //
 // Scheduling: the work units (item, tile) of expert e are numbered tile-major (all items of
 // one weight tile are consecutive); the items sharing a weight tile run together on one XCD
-// and reuse it from L2 (the static blocks follow this numbering, the per-XCD lists take an
-// expert's units on their XCD item by item).
+// and reuse it from L2 (the work runs follow this numbering, the per-XCD lists take an
+// expert's units on their XCD item by item). A work-group claims its next unit on a 64-bit
+// per-XCD counter while its current unit runs; the experts' item geometry is read once per
+// launch into lane registers, so a unit's setup makes no dependent memory round trip.
 //   Per-XCD lists (GEMM1; GEMM2 with items of up to 128 rows): XCD x takes weight tiles
 //          t0, t0 + 8, .. of every expert, t0 = (x - 4 * (rank % 2)) % 8 for the expert's rank
 //          by descending item rows, so that every XCD gets the same mix of long and short
-//          units; its work-groups take the units of that list, longest experts first, from a
-//          per-XCD counter as they finish. Inside an expert the list goes item by item (the
+//          units; its work-groups take the units of that list, longest experts first, from the
+//          XCD's counter as they finish. Inside an expert the list goes item by item (the
 //          item's 2 GEMM1 or 3-4 GEMM2 tiles of this XCD, then the next item's), so that the
 //          units running together share their items' activation rows as well as their weight
 //          tiles: on the skewed T=4096 batch (experts of 26 items) GEMM1 fetches 2.34 instead
@@ -51,9 +53,19 @@
 //          contiguous blocks of units per XCD: GEMM1 296 against 313 us at T=8192, 164
 //          against 174 at T=1024, 656 against 682 on the skewed T=4096 batch; GEMM2 +
 //          combine 114 against 123 us at T=1024.
-//   Static blocks (GEMM2 with items of up to 160 rows): the units are dealt to the 8 XCDs in
-//          contiguous blocks, a work-group's units fixed in advance (the lists measured 253
-//          against 247 us at T=8192 and 573 against 552 on the skewed batch).
+//   Work runs with stealing (GEMM2 with items of up to 160 rows): XCD x owns a contiguous run
+//          of the unit numbering, cut at weight-tile boundaries where the estimated work (item
+//          rows plus a fixed cost per unit) reaches x/8 and (x+1)/8 of the launch's; its
+//          work-groups claim the run's units in order from the front of the XCD's counter.
+//          Once a run is used up its work-groups take units from the back of the run with the
+//          most units left: the counter's high half counts those, and a claim is good while
+//          the two halves together stay below the run's length, so every unit runs exactly
+//          once. Against contiguous equal blocks of units fixed in advance: GEMM2 + combine
+//          234.8 against 239.7 us at T=8192 (the XCDs end within 10 us of each other instead of
+//          28), 542 against 537 us on the skewed batch, whose GEMM1 gains 3 us from the unit
+//          setup without memory round trips. The cut estimate alone, without stealing, measured
+//          +13 us on the skewed batch: the XCDs' unit times differ by 5% with the load on their
+//          L2s, which no estimate made before the launch knows.
 #include <atomic>
 
 #include "moe_internal.h"
@@ -125,6 +137,9 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt(N | (7 << 4) | (15 << 8));
 }
 
+// waits for this wave's LDS operations only (vmcnt 63, expcnt 7, lgkmcnt 0)
+__device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (3 << 14)); }
+
 template <int ROWS>
 struct TileStage {
   uint8_t w[kTileW * 128];
@@ -139,7 +154,9 @@ struct TileStage {
 template <int ROWS>
 struct TileShared {
   TileStage<ROWS> st[kStages];
-  int next;
+  unsigned long long next;   // the claim counter's value before this work-group's last claim
+  int stolen;                // a unit taken from another XCD's run, or -1
+  int steal_from;            // that XCD
 };
 static_assert(sizeof(TileShared<kTileItemRowsLarge>) <= 160 * 1024 && sizeof(TileShared<kTileItemRowsMid>) <= 160 * 1024,
               "LDS of one CU");
@@ -183,7 +200,7 @@ __device__ __forceinline__ v8i lds_frag32(const uint8_t* buf, int m, int hh, int
 template <bool G1, int NG, int ROWS>
 __device__ __forceinline__ void tile_body(const GemmParams& p, const TileCtx<ROWS>& c, const TileCtx<ROWS>& n,
                                           bool have_n, int s_base, bool pre, TileShared<ROWS>& sh,
-                                          int32_t* queue) {
+                                          unsigned long long* claim, unsigned long long inc) {
   using S = TileShape<ROWS>;
   constexpr int KS = G1 ? kHBlocks : kIBlocks;
   // GEMM2 with two activation scales per K-step (64-column requantisation blocks): 32x32x64
@@ -382,8 +399,11 @@ __device__ __forceinline__ void tile_body(const GemmParams& p, const TileCtx<ROW
 #pragma nounroll
   for (int k = 0; k < KS; ++k) {
     // step k's loads are complete for this wave (only step k+1's may be in flight), and
-    // after the barrier for every wave; every wave is also done with stage s_next (step k-1)
-    wait_vmcnt<S::kLoadsPerStep>();
+    // after the barrier for every wave; every wave is also done with stage s_next (step k-1).
+    // A prefetched unit's first two steps landed before the previous unit's epilogue stored
+    // anything (below): those steps do not wait, so the stores drain under their MFMAs (the
+    // counter is in order, a wait for a later load waits for them).
+    if (!pre || k >= 2) wait_vmcnt<S::kLoadsPerStep>();
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __builtin_amdgcn_s_barrier();
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
@@ -415,10 +435,10 @@ __device__ __forceinline__ void tile_body(const GemmParams& p, const TileCtx<ROW
   // The loads in flight now are the next unit's first two steps, or reloads nobody reads; the
   // reloads must land before the next unit refills the ring.
   if (G1 || !have_n) wait_vmcnt<0>();
-  // the work-group's next list entry (per-XCD lists); the counter's round trip overlaps the
-  // epilogue
-  int got = 0;
-  if (queue != nullptr && threadIdx.x == 0) got = atomicAdd(queue, 1);
+  // the work-group's next claim on a per-XCD counter (front or back); the counter's round trip
+  // overlaps the epilogue
+  unsigned long long got = 0;
+  if (claim != nullptr && threadIdx.x == 0) got = atomicAdd(claim, inc);
 
   if constexpr (G1) {
     // SwiGLU (kernel.py:126-129) and requantisation per S::kQCols columns (kernel.py:131-135):
@@ -486,7 +506,10 @@ __device__ __forceinline__ void tile_body(const GemmParams& p, const TileCtx<ROW
       dest[g] = p.row_dest[pr];
       wt[g] = p.sorted_weight[pr];
     }
-    if (queue != nullptr && threadIdx.x == 0) sh.next = got;
+    // every load of this wave has landed, the next unit's first two steps (issued before
+    // these) included, before the first store
+    wait_vmcnt<0>();
+    if (claim != nullptr && threadIdx.x == 0) sh.next = got;
     auto store4 = [&](bool direct, int t, size_t slot, int h, const v4f& val) __attribute__((always_inline)) {
       if (direct) {
         if (p.out_dtype == MOE_FP8_OUT_BF16)
@@ -522,43 +545,70 @@ __device__ __forceinline__ void tile_body(const GemmParams& p, const TileCtx<ROW
       }
     }
   }
-  if (G1 && queue != nullptr && threadIdx.x == 0) sh.next = got;
+  if (G1 && claim != nullptr && threadIdx.x == 0) sh.next = got;
 }
 
 // NG (row groups of this wave's half) as a template argument: instantiations 0..kMaxNG.
 template <bool G1, int ROWS, int NG = 0>
 __device__ __forceinline__ void tile_body_ng(const GemmParams& p, const TileCtx<ROWS>& c, const TileCtx<ROWS>& n,
                                              bool have_n, int s_base, bool pre, TileShared<ROWS>& sh,
-                                             int32_t* queue) {
+                                             unsigned long long* claim, unsigned long long inc) {
   constexpr int kMax = (!G1 && TileShape<ROWS>::kW32) ? TileShape<ROWS>::kMaxNG32 : TileShape<ROWS>::kMaxNG;
   if constexpr (NG < kMax) {
-    if (c.ng == NG) tile_body<G1, NG, ROWS>(p, c, n, have_n, s_base, pre, sh, queue);
-    else tile_body_ng<G1, ROWS, NG + 1>(p, c, n, have_n, s_base, pre, sh, queue);
+    if (c.ng == NG) tile_body<G1, NG, ROWS>(p, c, n, have_n, s_base, pre, sh, claim, inc);
+    else tile_body_ng<G1, ROWS, NG + 1>(p, c, n, have_n, s_base, pre, sh, claim, inc);
   } else {
-    tile_body<G1, NG, ROWS>(p, c, n, have_n, s_base, pre, sh, queue);
+    tile_body<G1, NG, ROWS>(p, c, n, have_n, s_base, pre, sh, claim, inc);
   }
 }
 
+// The experts of the order the dispatch recorded (descending item rows, experts with items
+// first), lane k < 32 of every wavefront holding the k-th: its first item and item count and
+// the geometry of its items (expert index, first row, rows of every item but the last, rows of
+// the last). Read once per launch, so that a work unit's item costs no memory round trip.
+struct ExpertTable {
+  int first, ne, e, r0, chunk, last;
+};
+
+__device__ __forceinline__ ExpertTable expert_table(const GemmParams& p, int n_items) {
+  const int lane = threadIdx.x & 63;
+  ExpertTable t;
+  const int ord = lane < kExpertsLocal ? p.counters[kCtrOrder + lane] : 0;
+  t.first = ord & 0xFFFF;
+  t.ne = ord >> 16;
+  if (t.first + t.ne > n_items) t.ne = 0;
+  const int4* wi = reinterpret_cast<const int4*>(p.work_items);
+  const int4 a = t.ne > 0 ? wi[t.first] : int4{0, 0, 0, 0};
+  t.last = t.ne > 0 ? wi[t.first + t.ne - 1].z : 0;
+  t.e = a.x;
+  t.r0 = a.y;
+  t.chunk = a.z;
+  return t;
+}
+
 // The pointers and item of work unit u for this lane (all of it wave-uniform but the DMA
-// offsets and the lane's block scales).
+// offsets and the lane's block scales). Unit u of the expert whose items start at item `first`
+// is (item first + v % items, weight tile v / items) with v = u - first * TILES.
 template <bool G1, int ROWS>
-__device__ __forceinline__ void unit_setup(const GemmParams& p, int u, TileCtx<ROWS>& c) {
+__device__ __forceinline__ void unit_setup(const GemmParams& p, const ExpertTable& tab, int u, TileCtx<ROWS>& c) {
   using S = TileShape<ROWS>;
   constexpr int TILES = (G1 ? 2 * kInter : kHidden) / kTileW;
   constexpr int KS = G1 ? kHBlocks : kIBlocks;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int q = u / TILES;
-  const int qw = reinterpret_cast<const int4*>(p.work_items)[q].w;
-  const int first = qw & 0xFFFF, ne = qw >> 16;
-  const int v = u - first * TILES;
-  const int4 it = reinterpret_cast<const int4*>(p.work_items)[first + v % ne];
-  // work-item fields are wave-uniform; say so, so that everything derived from them
-  // (notably the weight block-scale addresses) stays in scalar registers
-  const int e = __builtin_amdgcn_readfirstlane(it.x);
-  c.r0 = __builtin_amdgcn_readfirstlane(it.y);
-  c.rows = __builtin_amdgcn_readfirstlane(it.z);
-  c.tile = __builtin_amdgcn_readfirstlane(v / ne);
+  const unsigned long long m = __ballot(lane < kExpertsLocal && tab.ne > 0 && u >= tab.first * TILES &&
+                                        u < (tab.first + tab.ne) * TILES);
+  // (a unit no expert holds cannot come from the lists; it would run as an empty item of
+  // expert 0, tile 0, rows from 0)
+  const int k = m != 0 ? __builtin_ctzll(m) : 0;
+  const int ne = m != 0 ? __builtin_amdgcn_readlane(tab.ne, k) : 1;
+  const int v = m != 0 ? u - __builtin_amdgcn_readlane(tab.first, k) * TILES : 0;
+  const int item = v % ne;
+  const int chunk = __builtin_amdgcn_readlane(tab.chunk, k);
+  const int e = m != 0 ? __builtin_amdgcn_readlane(tab.e, k) : 0;
+  c.r0 = m != 0 ? __builtin_amdgcn_readlane(tab.r0, k) + item * chunk : 0;
+  c.rows = m == 0 ? 0 : item == ne - 1 ? __builtin_amdgcn_readlane(tab.last, k) : chunk;
+  c.tile = v / ne;
 
   c.wbase = G1 ? p.w13 : p.w2;
   // DMA j of this wave fills 8 tile rows, lane l writing row +l/8, physical chunk l%8
@@ -644,13 +694,11 @@ struct XcdList {
 };
 
 template <int TILES>
-__device__ __forceinline__ XcdList<TILES> xcd_list(const GemmParams& p, int x, int n_items) {
+__device__ __forceinline__ XcdList<TILES> xcd_list(const ExpertTable& tab, int x) {
   XcdList<TILES> l;
   const int lane = threadIdx.x & 63;
-  const int ord = lane < kExpertsLocal ? p.counters[kCtrOrder + lane] : 0;
-  l.first = ord & 0xFFFF;
-  l.ne = ord >> 16;
-  if (l.first + l.ne > n_items) l.ne = 0;
+  l.first = tab.first;
+  l.ne = tab.ne;
   l.t0 = (x - 4 * (lane & 1)) & 7;
   const int len = ((TILES - l.t0 + 7) >> 3) * l.ne;
   int incl = len;
@@ -664,86 +712,229 @@ __device__ __forceinline__ XcdList<TILES> xcd_list(const GemmParams& p, int x, i
   return l;
 }
 
+// GEMM2 with 160-row items: XCD v owns a contiguous run of the tile-major unit numbering (all
+// items of one weight tile consecutive), [cut v, cut v+1). Cut v is the unit where the
+// estimated work of the units before it reaches v/8 of the launch's, rounded down to a weight-
+// tile boundary (cut 8: the end); a unit's estimate is its item rows plus kUnitFixedRows. Lane
+// v < 8 of every wavefront holds run v. The items sharing a weight tile run together on one XCD
+// and reuse the tile from its L2.
+struct RangeSet {
+  int begin, total;
+  __device__ __forceinline__ int begin_of(int v) const { return __builtin_amdgcn_readlane(begin, v); }
+  __device__ __forceinline__ int total_of(int v) const { return __builtin_amdgcn_readlane(total, v); }
+};
+
+// One XCD's run as a list: entry j is unit begin + j.
+struct RangeList {
+  int begin, total;
+  __device__ __forceinline__ bool entry(int j, int& u) const {
+    if (j >= total) return false;
+    u = begin + j;
+    return true;
+  }
+};
+
+// Estimated fixed cost of a GEMM2 unit with 160-row items, in item rows: streaming its
+// 256 x 2048 weight tile (units took 15.5 us + 0.078 us per item row at T=8192 and
+// 16.6 + 0.05 on the skewed T=4096 batch).
+constexpr int kUnitFixedRows = 256;
+
+// The runs from the expert table (exact integer sums, so that the experts' ranges of the work
+// tile it; every work-group computes the same cuts).
+template <int TILES>
+__device__ __forceinline__ RangeSet range_set(const ExpertTable& tab, int n_items) {
+  const int lane = threadIdx.x & 63;
+  const bool has = lane < kExpertsLocal && tab.ne > 0;
+  const int rows = has ? (tab.ne - 1) * tab.chunk + tab.last : 0;
+  const long long per_tile = has ? (long long)kUnitFixedRows * tab.ne + rows : 0;
+  const long long work = per_tile * TILES;
+  // the work of the experts whose items come before this one's, and of all
+  long long before = 0, total = 0;
+  for (int k = 0; k < kExpertsLocal; ++k) {
+    const int fk = __builtin_amdgcn_readlane(tab.first, k);
+    const long long wk = ((long long)__builtin_amdgcn_readlane((int)(work >> 32), k) << 32) |
+                         (uint32_t)__builtin_amdgcn_readlane((int)work, k);
+    total += wk;
+    before += fk < tab.first ? wk : 0;
+  }
+  int cut = n_items * TILES;
+  for (int v = 0; v < 8; ++v) {
+    const long long target = (total * v) >> 3;
+    const unsigned long long m = __ballot(has && before <= target && target < before + work);
+    if (m != 0) {
+      const int k = __builtin_ctzll(m);
+      const long long off = target - __shfl(before, k);
+      const long long pt = __shfl(per_tile, k);
+      // floor(off / pt) < TILES: a float quotient, then corrected exactly
+      int t = min((int)((float)off / (float)pt), TILES - 1);
+      while (t > 0 && (long long)t * pt > off) --t;
+      while (t < TILES - 1 && (long long)(t + 1) * pt <= off) ++t;
+      const int u = __builtin_amdgcn_readlane(tab.first, k) * TILES + t * __builtin_amdgcn_readlane(tab.ne, k);
+      if (lane == v) cut = u;
+    } else if (lane == v) {
+      cut = v == 0 ? 0 : n_items * TILES;
+    }
+  }
+  // every run stays inside [0, units)
+  cut = min(max(cut, 0), n_items * TILES);
+  RangeSet r;
+  r.begin = cut;
+  r.total = max(__shfl_down(cut, 1) - cut, 0);
+  return r;
+}
+
+// The claim counters: one 64-bit counter per XCD and kernel, whose low half counts the claims
+// of the XCD's own work-groups on its list (from the front, after the 1 (GEMM1) or 2 (GEMM2)
+// entries per work-group handed out up front) and whose high half counts the units other
+// XCDs' work-groups took from the back of its run. Every claim adds to one half and sees both:
+// a claim is good while pre + front + back < the list's length, so the front and back claims
+// never meet, and one that fails marks the list used up for good.
+struct Claim {
+  int front, back;
+};
+__device__ __forceinline__ Claim claim_of(unsigned long long o) {
+  return Claim{(int)__builtin_amdgcn_readfirstlane((uint32_t)o), (int)__builtin_amdgcn_readfirstlane((uint32_t)(o >> 32))};
+}
+
 template <bool G1, int ROWS>
 __global__ __launch_bounds__(kTileWaves * 64, 1) void gemm_tile_kernel(GemmParams p) {
   constexpr int TILES = (G1 ? 2 * kInter : kHidden) / kTileW;
   constexpr int KS = G1 ? kHBlocks : kIBlocks;
+  // GEMM2 with 160-row items: work-groups whose XCD's run is used up take units from the
+  // back of other XCDs' runs
+  constexpr bool kSteal = !G1 && ROWS == kTileItemRowsLarge;
   __shared__ __attribute__((aligned(1024))) TileShared<ROWS> sh;
 
   const int n_items = min(p.counters[kCtrItems], p.max_items);
-  if constexpr (G1 || ROWS == kTileItemRowsMid) {
-    // XCD x = blockIdx.x % 8 (the grid is a multiple of 8): a work-group starts on list entry
-    // blockIdx.x / 8 (GEMM2: and reserves blockIdx.x / 8 + per_xcd) and takes each later one
-    // from the XCD's counter (restarted by the dispatch), offset by the entries handed out
-    // up front. All waves of a work-group see the same entries, so all leave together.
-    const int x = blockIdx.x & 7;
-    const XcdList<TILES> list = xcd_list<TILES>(p, x, n_items);
-    int32_t* queue = p.counters + kCtrQueue + (G1 ? 0 : 8) + x;
-    const int per_xcd = gridDim.x >> 3;
+  // XCD x = blockIdx.x % 8 (the grid is a multiple of 8): a work-group starts on list entry
+  // blockIdx.x / 8 (GEMM2: and reserves blockIdx.x / 8 + per_xcd) and takes each later one
+  // with a claim on the XCD's counter (restarted after the launch), offset by the entries
+  // handed out up front. All waves of a work-group see the same entries, so all leave together.
+  const int x = blockIdx.x & 7;
+  const int lane = threadIdx.x & 63;
+  const int per_xcd = gridDim.x >> 3;
+  const int pre = (G1 ? 1 : 2) * per_xcd;
+  unsigned long long* const claims = reinterpret_cast<unsigned long long*>(p.counters + kCtrClaim) + (G1 ? 0 : 8);
+  const ExpertTable tab = expert_table(p, n_items);
+  auto run_list = [&](const auto& list, const RangeSet& ranges) __attribute__((always_inline)) {
+    int src = x;   // the XCD whose counter the work-group claims on (the own one: its front)
+    // a unit from the back of another XCD's run, the one with the most units left by a read
+    // of all eight counters (wavefront 0 claims, the work-group reads the result); false once
+    // every run is used up. A claim that fails leaves its run used up, so this takes at most
+    // eight claims.
+    auto steal = [&](int& u) __attribute__((always_inline)) -> bool {
+      if constexpr (!kSteal) {
+        return false;
+      } else {
+        if (threadIdx.x < 64) {
+          int got = -1, from = x;
+          for (int attempt = 0; attempt < 8; ++attempt) {
+            const unsigned long long o =
+                lane < 8 ? __hip_atomic_load(claims + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0;
+            const int left = lane < 8 && lane != x
+                                 ? ranges.total - pre - (int)(uint32_t)o - (int)(uint32_t)(o >> 32) : 0;
+            int v = -1, most = 0;
+            for (int k = 0; k < 8; ++k) {
+              const int lk = __builtin_amdgcn_readlane(left, k);
+              if (lk > most) {
+                most = lk;
+                v = k;
+              }
+            }
+            if (v < 0) break;
+            unsigned long long c = 0;
+            if (lane == 0) c = atomicAdd(claims + v, 1ull << 32);
+            const Claim cl = claim_of(c);
+            const int tv = ranges.total_of(v);
+            if (pre + cl.front + cl.back < tv) {
+              got = ranges.begin_of(v) + tv - 1 - cl.back;
+              from = v;
+              break;
+            }
+          }
+          if (lane == 0) {
+            sh.stolen = got;
+            sh.steal_from = from;
+          }
+        }
+        wait_lgkmcnt0();
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_s_barrier();
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        u = __builtin_amdgcn_readfirstlane(sh.stolen);
+        src = __builtin_amdgcn_readfirstlane(sh.steal_from);
+        return u >= 0;
+      }
+    };
+    // the unit of the claim made during the last unit (or a stolen one)
+    auto claimed = [&](int& u) __attribute__((always_inline)) -> bool {
+      const Claim cl = claim_of(sh.next);
+      if (src == x) {
+        if (pre + cl.front + cl.back < list.total) return list.entry(pre + cl.front, u);
+      } else {
+        const int tv = ranges.total_of(src);
+        if (pre + cl.front + cl.back < tv) {
+          u = ranges.begin_of(src) + tv - 1 - cl.back;
+          return true;
+        }
+      }
+      return steal(u);
+    };
     int u;
-    if (list.entry(blockIdx.x >> 3, u)) {
+    bool have_c = list.entry(blockIdx.x >> 3, u);
+    if (!have_c) have_c = steal(u);
+    if (have_c) {
       TileCtx<ROWS> c, n;
-      unit_setup<G1, ROWS>(p, u, c);
+      unit_setup<G1, ROWS>(p, tab, u, c);
       bool have_n = false;
-      if constexpr (!G1) have_n = list.entry(per_xcd + (blockIdx.x >> 3), u);
-      if (have_n) unit_setup<G1, ROWS>(p, u, n);
+      if constexpr (!G1) {
+        have_n = list.entry(per_xcd + (blockIdx.x >> 3), u);
+        if (!have_n) have_n = steal(u);
+      }
+      if (have_n) unit_setup<G1, ROWS>(p, tab, u, n);
       else n = c;
       int s_base = 0;
-      bool pre = false;
+      bool pre_loaded = false;
       for (;;) {
-        tile_body_ng<G1, ROWS>(p, c, n, have_n, s_base, pre, sh, queue);
-        __syncthreads();
-        const int j = (G1 ? 1 : 2) * per_xcd + __builtin_amdgcn_readfirstlane(sh.next);
+        // GEMM2 claims the entry after the reserved one only while there is one
+        const bool claim_now = G1 || have_n;
+        tile_body_ng<G1, ROWS>(p, c, n, have_n, s_base, pre_loaded, sh, claim_now ? claims + src : nullptr,
+                               src == x ? 1ull : 1ull << 32);
+        // publishes sh.next (LDS); the unit's global stores may still be in flight
+        wait_lgkmcnt0();
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_s_barrier();
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
         if constexpr (G1) {
-          if (!list.entry(j, u)) break;
-          unit_setup<G1, ROWS>(p, u, c);
+          if (!claimed(u)) break;
+          unit_setup<G1, ROWS>(p, tab, u, c);
         } else {
           if (!have_n) break;
           c = n;
-          have_n = list.entry(j, u);
-          if (have_n) unit_setup<G1, ROWS>(p, u, n);
+          have_n = claimed(u);
+          if (have_n) unit_setup<G1, ROWS>(p, tab, u, n);
           else n = c;
-          pre = true;
+          pre_loaded = true;
         }
         s_base = (s_base + KS) % kStages;
       }
     }
-    // The XCD's last work-group to leave restarts its counters, so that a launch of this
-    // stage alone finds them at zero too: every other work-group's last entry has returned
-    // before it counted itself out.
+    // The last work-group of the grid to leave restarts the claim counters, so that the next
+    // launch finds them at zero: every other work-group's last claim has returned before it
+    // counted itself out.
     if (threadIdx.x == 0) {
-      int32_t* left = p.counters + kCtrLeft + (G1 ? 0 : 8) + x;
-      if (atomicAdd(left, 1) == per_xcd - 1) {
-        atomicExch(queue, 0);
+      int32_t* left = p.counters + kCtrLeft + (G1 ? 0 : 1);
+      if (atomicAdd(left, 1) == (int)gridDim.x - 1) {
+        for (int v = 0; v < 8; ++v) atomicExch(claims + v, 0ull);
         atomicExch(left, 0);
       }
     }
+  };
+  if constexpr (kSteal) {
+    const RangeSet ranges = range_set<TILES>(tab, n_items);
+    run_list(RangeList{ranges.begin_of(x), ranges.total_of(x)}, ranges);
   } else {
-    const int units = n_items * TILES;
-    const int per_xcd = (units + 7) >> 3;
-    // slot w of the static schedule: unit (w % 8) * per_xcd + w / 8 (consecutive slots go to
-    // different XCDs, each XCD's units are one contiguous range); a work-group takes slots
-    // blockIdx.x, + gridDim.x, .. (a multiple of 8: always the same XCD), and once a slot's
-    // unit is past the end so are all its later ones
-    auto unit_of = [&](int w) { return (w & 7) * per_xcd + (w >> 3); };
-    int w = blockIdx.x;
-    if (w >= 8 * per_xcd || unit_of(w) >= units) return;
-    TileCtx<ROWS> c, n;
-    unit_setup<G1, ROWS>(p, unit_of(w), c);
-    int s_base = 0;
-    bool pre = false;
-    for (;;) {
-      const int wn = w + gridDim.x;
-      const bool have_n = wn < 8 * per_xcd && unit_of(wn) < units;
-      if (have_n) unit_setup<G1, ROWS>(p, unit_of(wn), n);
-      else n = c;
-      tile_body_ng<G1, ROWS>(p, c, n, have_n, s_base, pre, sh, nullptr);
-      if (!have_n) break;
-      w = wn;
-      c = n;
-      s_base = (s_base + KS) % kStages;
-      pre = true;
-    }
+    run_list(xcd_list<TILES>(tab, x), RangeSet{0, 0});
   }
 }
 

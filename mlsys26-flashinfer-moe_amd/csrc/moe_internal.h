@@ -49,12 +49,12 @@ constexpr int kFusedDispatchTokens = 64;
 // Control block (workspace counters[]).
 constexpr int kCtrItems = 0;    // number of GEMM work items
 constexpr int kCtrAssign = 1;   // N, the number of local assignments
-constexpr int kCtrQueue = 16;   // [2][8] per-XCD unit counters of the GEMM1 and GEMM2 tile kernels
-constexpr int kCtrLeft = 32;    // [2][8] their work-groups per XCD that have left
-constexpr int kCtrOrder = 48;   // [32] experts by descending item rows: first item | items << 16
-constexpr int kNumCounters = 80;
-static_assert(kCtrQueue + 16 <= kCtrLeft && kCtrLeft + 16 <= kCtrOrder && kCtrOrder + kExpertsLocal <= kNumCounters,
-              "control block");
+constexpr int kCtrClaim = 16;   // [2][8] 64-bit per-XCD claim counters of the GEMM1 and GEMM2 tile kernels
+constexpr int kCtrLeft = 48;    // [2] their work-groups that have left
+constexpr int kCtrOrder = 64;   // [32] experts by descending item rows: first item | items << 16
+constexpr int kNumCounters = 96;
+static_assert(kCtrClaim % 2 == 0 && kCtrClaim + 32 <= kCtrLeft && kCtrLeft + 2 <= kCtrOrder &&
+              kCtrOrder + kExpertsLocal <= kNumCounters, "control block");
 
 // Rows of a work item of the tile GEMMs: gemm_tile_kernel has an instance for items of up to
 // 128 rows and one for items of up to 160 (10 row groups of 16, the largest whose ring fits LDS).
@@ -127,7 +127,7 @@ struct GemmParams {
   int T;
   int max_items;
   const int32_t* work_items;
-  int32_t* counters;           // read-only but for the tile kernels' unit counters
+  int32_t* counters;           // read-only but for the tile kernels' claim counters
   const int32_t* sorted_token;
   const float* sorted_weight;
   const int32_t* sorted_slot;

@@ -367,7 +367,7 @@ __device__ __forceinline__ void finish_counts(const RouteParams& p, int e, int r
   }
   if (e == kExpertsLocal - 1) p.counters[kCtrItems] = ich;
   // The order in which the tile kernels' per-XCD lists visit the experts: by descending item
-  // rows (ties by expert index), experts without rows last. Their unit counters restart.
+  // rows (ties by expert index), experts without rows last. Their claim counters restart.
   const int key = nch > 0 ? min(chunk, run) : 0;
   int rank = 0;
   for (int o = 0; o < kExpertsLocal; ++o) {
@@ -375,10 +375,8 @@ __device__ __forceinline__ void finish_counts(const RouteParams& p, int e, int r
     rank += (ko > key || (ko == key && o < e)) ? 1 : 0;
   }
   p.counters[kCtrOrder + rank] = first | (nch << 16);
-  if (e < 16) {
-    p.counters[kCtrQueue + e] = 0;
-    p.counters[kCtrLeft + e] = 0;
-  }
+  p.counters[kCtrClaim + e] = 0;
+  if (e < 2) p.counters[kCtrLeft + e] = 0;
 }
 
 }  // namespace

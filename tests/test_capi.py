@@ -61,7 +61,7 @@ def test_layout_consistent(pkg, T):
         ("expert_start", 4 * 33), ("sorted_token", 4 * 8 * T), ("sorted_weight", 4 * 8 * T),
         ("sorted_slot", 4 * 8 * T), ("token_nlocal", 4 * T), ("slot_rank", 4 * 8 * T),
         ("block_count", 4 * 32 * L.route_blocks), ("work_items", 16 * L.max_work_items),
-        ("counters", 4 * 80), ("act", 8 * T * 2048), ("act_scale", 4 * 8 * T * 2048 // 64),
+        ("counters", 4 * 96), ("act", 8 * T * 2048), ("act_scale", 4 * 8 * T * 2048 // 64),
         ("partial", 0 if decode else 4 * 8 * T * 7168),
         ("swiglu", 4 * 8 * T * 2048 if L.rows_per_item <= 32 else 0), ("row_dest", 4 * 8 * T),
     ]

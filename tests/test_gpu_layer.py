@@ -296,7 +296,7 @@ def test_intermediate_fp8_matches_oracle(name):
 
 @pytest.mark.parametrize("name", ["t1024_off64", "t4096_skew"])
 def test_tile_stage_repeated(name):
-    """The GEMM1 tile kernel takes its units from per-XCD counters that the dispatch restarts.
+    """The GEMM1 tile kernel claims its units on per-XCD counters that the dispatch restarts.
     GEMM1 launched again after its result was wiped (no dispatch in between) redoes every unit:
     the launch before left the counters restarted. Staged and whole-layer runs agree bitwise."""
     gh = _gh()
@@ -317,6 +317,31 @@ def test_tile_stage_repeated(name):
     gh.gemm2_combine(args, ws)
     torch.cuda.synchronize()
     assert torch.equal(whole.view(torch.int16), out.view(torch.int16)), "staged and whole-layer runs differ"
+
+
+@pytest.mark.parametrize("name", ["t1024_off64", "t4096_skew"])
+def test_gemm2_stage_repeated(name):
+    """The GEMM2 tile kernel claims its units on per-XCD counters (above 4096 tokens also from
+    the back of other XCDs' runs) that the last work-group of a launch restarts. GEMM2 and the
+    combine launched twice after one dispatch and GEMM1, the output wiped in between, give the
+    whole layer's bits both times: the second launch found every unit unclaimed."""
+    gh = _gh()
+    kw, _ = _workload(name)
+    T = kw["routing_logits"].shape[0]
+    print(f"gemm2 stage repeated {name} T={T}", flush=True)
+    whole = _run_full(kw)
+    dev = kw["routing_logits"].device
+    out = torch.full((T, 7168), float("nan"), dtype=torch.bfloat16, device=dev)
+    ws = gh.new_workspace(T, dev)
+    assert ws.layout.rows_per_item > 32
+    args = gh.make_args(**kw, output=out)
+    gh.route_dispatch(args, ws)
+    gh.gemm1(args, ws)
+    for rep in range(2):
+        out.fill_(float("nan"))
+        gh.gemm2_combine(args, ws)
+        torch.cuda.synchronize()
+        assert torch.equal(whole.view(torch.int16), out.view(torch.int16)), f"launch {rep} differs"
 
 
 @pytest.mark.parametrize("name", ["t1024_off64", "t4096_skew"])
