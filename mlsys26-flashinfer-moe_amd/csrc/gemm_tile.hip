@@ -460,7 +460,7 @@ __device__ __forceinline__ void tile_body(const GemmParams& p, const TileCtx<ROW
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const float x1 = acc[h][g][i], x2 = acc[2 + h][g][i];
-          cval[g][h][i] = (x2 / (1.0f + __expf(-x2))) * x1;
+          cval[g][h][i] = x2 * __builtin_amdgcn_rcpf(1.0f + __expf(-x2)) * x1;
           amax = fmaxf(amax, fabsf(cval[g][h][i]));
         }
       amax = fmaxf(amax, __shfl_xor(amax, 16));
@@ -475,12 +475,13 @@ __device__ __forceinline__ void tile_body(const GemmParams& p, const TileCtx<ROW
                              ? fmaxf(amax_buf[wb & 2][m], amax_buf[(wb & 2) + 1][m])
                              : fmaxf(fmaxf(amax_buf[0][m], amax_buf[1][m]), fmaxf(amax_buf[2][m], amax_buf[3][m]));
       const float scale = fmaxf(amax / 448.0f, 1e-12f);
+      const float inv = __builtin_amdgcn_rcpf(scale);
       if (m < c.rows) {
         uint8_t* dst = p.act + (size_t)(c.r0 + m) * kInter + c.tile * 128 + 32 * wb + 4 * (lane >> 4);
 #pragma unroll
         for (int h = 0; h < 2; ++h)
           *reinterpret_cast<uint32_t*>(dst + 16 * h) =
-              pack_fp8x4(cval[g][h][0] / scale, cval[g][h][1] / scale, cval[g][h][2] / scale, cval[g][h][3] / scale);
+              pack_fp8x4(cval[g][h][0] * inv, cval[g][h][1] * inv, cval[g][h][2] * inv, cval[g][h][3] * inv);
         // the first wave of each scale block writes the block's scale
         if ((wb & (S::kQCols / 32 - 1)) == 0 && lane < 16)
           p.act_scale[(size_t)(c.r0 + m) * S::kQBlocks + (c.tile * 128 + 32 * wb) / S::kQCols] = scale;
