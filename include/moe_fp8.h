@@ -116,7 +116,7 @@ typedef struct moe_fp8_args {
  *   slot_rank     int32 [T*8]       internal: the multi-work-group dispatch's stable ranks
  *   work_items    int32 [max_items, 4]  GEMM work list (expert, first row, rows,
  *                                   first item of the expert | its item count << 16) (kernel.py:384-407)
- *   counters      int32 [80]        [0] number of work items, [1] N; the rest internal
+ *   counters      int32 [96]        [0] number of work items, [1] N; the rest internal
  *                                   (the tile kernels' work-list state)
  *   act           fp8   [N_max, 2048]    SwiGLU output requantised to e4m3fn          (kernel.py:669)
  *   act_scale     fp32  [N_max, 32]    its 1 x requant_block scales, row-major per row,
