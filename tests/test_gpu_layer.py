@@ -533,6 +533,13 @@ def _given_topk(case, T, rng):
     elif case == "repeat":                       # a token naming one local expert twice
         ids[:, 0] = rng.integers(0, 32, size=T)
         ids[:, 1] = ids[:, 0]
+    elif case == "two_experts":
+        # above 4096 tokens: every token on local expert 3 or 29, a sixth of them on both
+        # (parked rows), nothing else local
+        ids = np.where(ids < 32, ids + 32, ids)
+        ids[: T // 2, 0] = 3
+        ids[T // 2:, 0] = 29
+        ids[T // 3: T // 2, 1] = 29
     elif case == "few_local":
         # large-T items of every shape: expert 5 with 300 rows (two items), expert 17 with
         # exactly 160 (one full item), expert 9 with 200 (two), expert 30 with 20; tokens
@@ -549,7 +556,8 @@ def _given_topk(case, T, rng):
 
 @pytest.mark.parametrize("T,case", [(1, "all_local"), (40, "repeat"), (64, "all_local"), (65, "repeat"), (256, "all_local"),
                                     (257, "all_local"), (600, "one_expert"), (600, "none_local"),
-                                    (4095, "all_local"), (4096, "all_local"), (4100, "few_local")])
+                                    (4095, "all_local"), (4096, "all_local"), (4100, "few_local"),
+                                    (6000, "one_expert"), (5000, "two_experts")])
 def test_layer_edge_cases_given_topk(T, case):
     """The GEMM stages on constructed top-k lists: one token, a repeated expert, every token
     on one expert (many items of one expert on the tile path), nothing local, the largest
@@ -557,7 +565,9 @@ def test_layer_edge_cases_given_topk(T, case):
     32-row-item batch (T=65), and at T >= 4096
     (items of up to 160 rows) items of every shape next to thousands of tokens without a
     local expert. T=257 is the first batch on the tile kernels; T=4095 and T=4096 put 1024 rows
-    on every local expert, the largest batch of 128-row items and the first of 160-row items."""
+    on every local expert, the largest batch of 128-row items and the first of 160-row items.
+    T=6000 on one expert and T=5000 on two make GEMM2's per-XCD runs split one expert's weight
+    tiles (and the units taken from the back of other runs come from the same expert)."""
     gh = _gh()
     dev = torch.device("cuda:0")
     w, wnp = _weights()
@@ -585,6 +595,8 @@ def test_layer_edge_cases_given_topk(T, case):
     tokens = None if T <= 40 else np.sort(rng.choice(T, 24, replace=False))
     if case == "few_local":   # every kind of token: 2 local experts, each item's edges, none
         tokens = np.unique(np.concatenate([tokens, [0, 39, 40, 299, 300, 459, 460, 479, 480, 639, 640, T - 1]]))
+    if case == "two_experts":   # both sides of each boundary between the token groups
+        tokens = np.unique(np.concatenate([tokens, [0, T // 3 - 1, T // 3, T // 2 - 1, T // 2, T - 1]]))
     emu = olayer.layer_forward(**npkw, mode="emulated", topk=(ids, tw), tokens=tokens, requant_block=_requant_block(T))
     sel = slice(None) if tokens is None else tokens
     if case == "none_local":
