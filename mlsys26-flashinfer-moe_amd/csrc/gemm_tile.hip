@@ -176,6 +176,11 @@ struct TileCtx {
                                // (GEMM1 gate) and 2,3 (GEMM1 up)
   int r0, rows, tile, m0;      // item rows [r0, r0+rows); first item row of this wave's half
   int ng;                      // row groups of this wave's half
+  // GEMM2: the destination (token, or -1 - flat slot) and routing weight of the lane's row in
+  // each of this wave's row groups, loaded when the unit is set up (a unit ahead) so that the
+  // epilogue makes no memory round trip for them (rows past the item read its first row)
+  int dest[TileShape<ROWS>::kW32 ? TileShape<ROWS>::kMaxNG32 : TileShape<ROWS>::kMaxNG];
+  float wt[TileShape<ROWS>::kW32 ? TileShape<ROWS>::kMaxNG32 : TileShape<ROWS>::kMaxNG];
 };
 
 // A 16-row MFMA operand fragment (rows m0 .. m0+15 of an LDS tile): lane l holds row
@@ -490,25 +495,15 @@ __device__ __forceinline__ void tile_body(const GemmParams& p, const TileCtx<ROW
     __syncthreads();
   } else {
     // Each row's destination as the dispatch wrote it (the token, or -1 - its flat slot) and its
-    // routing weight: two independent loads per row group, all issued before the first store, so
-    // that one round trip covers them and the list entry taken above (a wait also waits for the
-    // next unit's prefetched K-steps: vmcnt counts in order; deriving the destination here from
-    // the token's local count took a second, dependent round trip). Rows past the item read its
-    // first row.
+    // routing weight come from the unit's set-up, a unit ahead (loaded here, they cost the
+    // epilogue a round trip).
     // (W32: the lane's row is c.m0 + 32g + lane%32, its 16 values four runs of 4 consecutive
     // hidden columns, 8q + 4(lane/32) .. +3 of each 32-row weight block)
     constexpr int kGRows = W32 ? 32 : 16;
-    int dest[NG > 0 ? NG : 1];
-    float wt[NG > 0 ? NG : 1];
-#pragma unroll
-    for (int g = 0; g < NG; ++g) {
-      const int m = c.m0 + kGRows * g + (lane & (kGRows - 1));
-      const int pr = c.r0 + (m < c.rows ? m : 0);
-      dest[g] = p.row_dest[pr];
-      wt[g] = p.sorted_weight[pr];
-    }
-    // every load of this wave has landed, the next unit's first two steps (issued before
-    // these) included, before the first store
+    const int* dest = c.dest;
+    const float* wt = c.wt;
+    // every load of this wave has landed, the next unit's first two steps included, before the
+    // first store
     wait_vmcnt<0>();
     if (claim != nullptr && threadIdx.x == 0) sh.next = got;
     auto store4 = [&](bool direct, int t, size_t slot, int h, const v4f& val) __attribute__((always_inline)) {
@@ -666,6 +661,16 @@ __device__ __forceinline__ void unit_setup(const GemmParams& p, const ExpertTabl
   const int g0 = (groups + 1) >> 1;
   c.ng = (wave >> 2) == 0 ? g0 : groups - g0;
   c.m0 = (wave >> 2) == 0 ? 0 : kGRows * g0;
+  if constexpr (!G1) {
+    constexpr int kMaxG = S::kW32 ? S::kMaxNG32 : S::kMaxNG;
+#pragma unroll
+    for (int g = 0; g < kMaxG; ++g) {
+      const int m = c.m0 + kGRows * g + (lane & (kGRows - 1));
+      const int pr = c.r0 + (m < c.rows ? m : 0);
+      c.dest[g] = p.row_dest[pr];
+      c.wt[g] = p.sorted_weight[pr];
+    }
+  }
 }
 
 // A per-XCD work list (see the top of the file). Lane k < 32 of every wavefront holds
