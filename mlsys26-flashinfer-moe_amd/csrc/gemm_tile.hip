@@ -506,38 +506,40 @@ __device__ __forceinline__ void tile_body(const GemmParams& p, const TileCtx<ROW
     // first store
     wait_vmcnt<0>();
     if (claim != nullptr && threadIdx.x == 0) sh.next = got;
-    auto store4 = [&](bool direct, int t, size_t slot, int h, const v4f& val) __attribute__((always_inline)) {
-      if (direct) {
-        if (p.out_dtype == MOE_FP8_OUT_BF16)
-          *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(p.out) + (size_t)t * kHidden + h) =
-              pack_bf16x4(val[0], val[1], val[2], val[3]);
-        else
-          *reinterpret_cast<v4f*>(reinterpret_cast<float*>(p.out) + (size_t)t * kHidden + h) = val;
-      } else {
-        *reinterpret_cast<v4f*>(p.partial + slot * kHidden + h) = val;
-      }
+    // The lane's 4-value runs of group g: run i at hidden column h0 + col(i) of the unit's tile,
+    // its values already weighted. Each group decides once where its row goes (the token's output
+    // row, bf16 or fp32, or the parked fp32 row), so that a row's stores share one branch.
+    constexpr int kRuns = W32 ? 8 : 4;
+    const int h0 = c.tile * kTileW + 64 * wb;
+    auto run_col = [&](int i) {
+      return W32 ? 32 * (i >> 2) + 8 * (i & 3) + 4 * (lane >> 5) : 16 * i + 4 * (lane >> 4);
     };
+    const bool bf16_out = p.out_dtype == MOE_FP8_OUT_BF16;
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
       const int m = c.m0 + kGRows * g + (lane & (kGRows - 1));
-      if (m < c.rows) {
-        const bool direct = dest[g] >= 0;
-        const int t = dest[g];
-        const size_t slot = (size_t)(-1 - dest[g]);
+      v4f val[kRuns];
+#pragma unroll
+      for (int i = 0; i < kRuns; ++i) {
         if constexpr (W32) {
-#pragma unroll
-          for (int blk = 0; blk < 2; ++blk)
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              const v16f& a = acc32[blk][g];
-              const v4f val = v4f{a[4 * q], a[4 * q + 1], a[4 * q + 2], a[4 * q + 3]} * wt[g];
-              store4(direct, t, slot, c.tile * kTileW + 64 * wb + 32 * blk + 8 * q + 4 * (lane >> 5), val);
-            }
+          const v16f& a = acc32[i >> 2][g];
+          const int q = i & 3;
+          val[i] = v4f{a[4 * q], a[4 * q + 1], a[4 * q + 2], a[4 * q + 3]} * wt[g];
         } else {
-#pragma unroll
-          for (int f = 0; f < 4; ++f)
-            store4(direct, t, slot, c.tile * kTileW + 64 * wb + 16 * f + 4 * (lane >> 4), acc[f][g] * wt[g]);
+          val[i] = acc[i][g] * wt[g];
         }
+      }
+      const int d = dest[g];
+      if (m < c.rows && d >= 0 && bf16_out) {
+        uint16_t* row = reinterpret_cast<uint16_t*>(p.out) + (size_t)d * kHidden + h0;
+#pragma unroll
+        for (int i = 0; i < kRuns; ++i)
+          *reinterpret_cast<uint2*>(row + run_col(i)) = pack_bf16x4(val[i][0], val[i][1], val[i][2], val[i][3]);
+      } else if (m < c.rows) {
+        float* row = (d >= 0 ? reinterpret_cast<float*>(p.out) + (size_t)d * kHidden
+                             : p.partial + (size_t)(-1 - d) * kHidden) + h0;
+#pragma unroll
+        for (int i = 0; i < kRuns; ++i) *reinterpret_cast<v4f*>(row + run_col(i)) = val[i];
       }
     }
   }
