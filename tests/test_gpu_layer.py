@@ -557,7 +557,7 @@ def _given_topk(case, T, rng):
 @pytest.mark.parametrize("T,case", [(1, "all_local"), (40, "repeat"), (64, "all_local"), (65, "repeat"), (256, "all_local"),
                                     (257, "all_local"), (600, "one_expert"), (600, "none_local"),
                                     (4095, "all_local"), (4096, "all_local"), (4100, "few_local"),
-                                    (6000, "one_expert"), (5000, "two_experts")])
+                                    (6000, "one_expert"), (5000, "two_experts"), (4200, "none_local")])
 def test_layer_edge_cases_given_topk(T, case):
     """The GEMM stages on constructed top-k lists: one token, a repeated expert, every token
     on one expert (many items of one expert on the tile path), nothing local, the largest
@@ -567,7 +567,8 @@ def test_layer_edge_cases_given_topk(T, case):
     local expert. T=257 is the first batch on the tile kernels; T=4095 and T=4096 put 1024 rows
     on every local expert, the largest batch of 128-row items and the first of 160-row items.
     T=6000 on one expert and T=5000 on two make GEMM2's per-XCD runs split one expert's weight
-    tiles (and the units taken from the back of other runs come from the same expert)."""
+    tiles (and the units taken from the back of other runs come from the same expert); T=4200
+    with nothing local leaves every run empty."""
     gh = _gh()
     dev = torch.device("cuda:0")
     w, wnp = _weights()
