@@ -724,8 +724,21 @@ __global__ __launch_bounds__(kSliceQuarters * 64) void gemm2_slice_kernel(GemmPa
         const int r0 = __builtin_amdgcn_readlane(my_item.y, it);
         const int rows = __builtin_amdgcn_readlane(my_item.z, it);
         const int r = r0 + (m < rows ? m : 0);
+        // The small loads first. The loop over items carries the ring slot that an item's last
+        // step fills with the next item's first step, and the compiler's copies of its scale
+        // registers at the back edge wait for those loads: issued ahead of the fragments, they
+        // leave the fragment loads in flight across the item boundary (packed weights; on the
+        // row-major weights the compiler still drains the ring there). Bit-identical; T=16
+        // GEMM2 stage 32.7-32.8 -> 32.3-32.5 us, T=64 about 0.3 us.
+#pragma unroll
+        for (int f = 0; f < kSliceF; ++f) {
+          const int orow = h0 + min(16 * f + 4 * (lane >> 4), kSliceRows - 1);   // first output row
+          g.sw[f] = p.w2_scale[((size_t)e * kHBlocks + orow / kBlock) * kIBlocks + ks];
+        }
+        g.sa = *reinterpret_cast<const float2*>(p.act_scale + (size_t)r * kQuantBlocks + 2 * ks);
+        g.tok = p.sorted_token[r];
+        g.wt = p.sorted_weight[r];
         if constexpr (!PACKED) {
-          // the DMAs first: the wait before the fragments are read counts the later loads
           uint8_t* dst = sh.ring[q] + (st % kSliceRing) * kSliceLdsStep;
 #pragma unroll
           for (int j = 0; j < kSliceLdsDma; ++j) {
@@ -736,21 +749,16 @@ __global__ __launch_bounds__(kSliceQuarters * 64) void gemm2_slice_kernel(GemmPa
                                              (lds_void_t*)(dst + j * 1024), 16, 0, 0);
           }
         }
+        if constexpr (PACKED) {
 #pragma unroll
-        for (int f = 0; f < kSliceF; ++f) {
-          // the lane's hidden row in fragment f (rows past the slice repeat its last row)
-          if constexpr (PACKED) {
+          for (int f = 0; f < kSliceF; ++f) {
+            // the lane's hidden row in fragment f (rows past the slice repeat its last row)
             const int hr = h0 + 16 * f + min(m, kSliceRows - 16 * f - 1);
             g.w[f] = load_frag_packed(p.w2 + (((size_t)e * (kHidden / 16) + (hr >> 4)) * kIBlocks + ks) * kPackedFrag +
                                       ((hr & 15) + 16 * (lane >> 4)) * 32);
           }
-          const int orow = h0 + min(16 * f + 4 * (lane >> 4), kSliceRows - 1);   // first output row
-          g.sw[f] = p.w2_scale[((size_t)e * kHBlocks + orow / kBlock) * kIBlocks + ks];
         }
         g.a = load_frag(p.act + (size_t)r * kInter + ks * 128 + (lane >> 4) * 16);
-        g.sa = *reinterpret_cast<const float2*>(p.act_scale + (size_t)r * kQuantBlocks + 2 * ks);
-        g.tok = p.sorted_token[r];
-        g.wt = p.sorted_weight[r];
       };
       SliceStage ring[kSliceRing];
 #pragma unroll
@@ -773,7 +781,9 @@ __global__ __launch_bounds__(kSliceQuarters * 64) void gemm2_slice_kernel(GemmPa
             // step st0 + u has landed once only the loads of the step just issued are in
             // flight: 4 DMAs, 2 weight scales, the act fragment (2) and its scales, plus the
             // rows' tokens and weights when that step is an item's last (the only step whose
-            // are read). Covering every load of step st0 + u here also keeps the compiler
+            // are read). The counts are exact (the compiled steps issue 9 and 11 loads): a
+            // step's DMAs follow its small loads, so a larger count could leave some of them
+            // in flight. Covering every load of step st0 + u here also keeps the compiler
             // from waiting on the rest itself, which it would do with vmcnt(0) while the
             // ring's DMAs are in flight.
             if (u == kSliceSteps - 2) wait_vm<kSliceLdsDma + 7>();
