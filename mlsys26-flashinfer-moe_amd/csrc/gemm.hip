@@ -121,15 +121,16 @@ struct StreamStage {
 // readlane, so the loop holds no branches and the compiler's waits cover exactly the step
 // being consumed. Lane l ends with rows 4*(l/16)+i of each weight fragment against row
 // l%16 of each row group.
-// With PACKED the weights come from the packed copy.
-template <int KIND, int NG, bool PACKED = false>
+// With PACKED the weights come from the packed copy. RING > 0 overrides the ring depth of the
+// kind (StreamShape::kRing).
+template <int KIND, int NG, bool PACKED = false, int RING = 0>
 __device__ __forceinline__ void stream_accumulate(const GemmParams& p, int e, int r0, int rows, int slice,
                                                   int lane, const int32_t* row_token,
                                                   v4f (&acc)[StreamShape<KIND>::kFrags][NG]) {
   using S = StreamShape<KIND>;
   constexpr int KS = S::kSteps;
   constexpr int NF = S::kFrags;
-  constexpr int NB = S::kRing;
+  constexpr int NB = RING > 0 ? RING : S::kRing;
   constexpr int KMAIN = KS - KS % NB;   // steps of the ring-unrolled main loop
   using SA = typename std::conditional<KIND == kG1, float, float2>::type;
   using Stage = StreamStage<NF, NG, SA>;
@@ -404,13 +405,13 @@ __device__ __forceinline__ v4f swiglu4(const v4f& x1, const v4f& x2) {
 // writes or parks the weighted rows.
 // GEMM1 on row-major weights streams them through the wavefront's LDS ring `ring`
 // (kNB * kG1LdsStep bytes); the other instances do not use it.
-template <int KIND, int NG, bool PACKED = false>
+template <int KIND, int NG, bool PACKED = false, int RING = 0>
 __device__ __forceinline__ void stream_unit(const GemmParams& p, int e, int r0, int rows, int slice, int lane,
                                             const int32_t* row_token, uint8_t* ring) {
   constexpr int NF = StreamShape<KIND>::kFrags;
   v4f acc[NF][NG];
   if constexpr (KIND == kG1 && !PACKED) stream_accumulate_g1_lds<NG>(p, e, r0, rows, slice, lane, row_token, ring, acc);
-  else stream_accumulate<KIND, NG, PACKED>(p, e, r0, rows, slice, lane, row_token, acc);
+  else stream_accumulate<KIND, NG, PACKED, RING>(p, e, r0, rows, slice, lane, row_token, acc);
   // lane: column (lane & 15) of each row group, fragment rows 4*(lane>>4) + i
 #pragma unroll
   for (int g = 0; g < NG; ++g) {
@@ -445,7 +446,7 @@ __device__ __forceinline__ void stream_unit(const GemmParams& p, int e, int r0, 
 
 // The work units of n_items items (item list and GEMM1's bucket-row -> token map in the
 // workspace, or in LDS for the fused dispatch below).
-template <int KIND, int MAXNG, bool PACKED = false>
+template <int KIND, int MAXNG, bool PACKED = false, int RING = 0>
 __device__ __forceinline__ void stream_units(const GemmParams& p, int n_items, const int4* items,
                                              const int32_t* row_token, uint8_t* ring) {
   constexpr int SL = StreamShape<KIND>::kSlices;
@@ -461,8 +462,8 @@ __device__ __forceinline__ void stream_units(const GemmParams& p, int n_items, c
     const int e = __builtin_amdgcn_readfirstlane(it.x);
     const int r0 = __builtin_amdgcn_readfirstlane(it.y);
     const int rows = __builtin_amdgcn_readfirstlane(it.z);
-    if (MAXNG == 1 || rows <= 16) stream_unit<KIND, 1, PACKED>(p, e, r0, rows, slice, lane, row_token, ring);
-    else stream_unit<KIND, MAXNG, PACKED>(p, e, r0, rows, slice, lane, row_token, ring);
+    if (MAXNG == 1 || rows <= 16) stream_unit<KIND, 1, PACKED, RING>(p, e, r0, rows, slice, lane, row_token, ring);
+    else stream_unit<KIND, MAXNG, PACKED, RING>(p, e, r0, rows, slice, lane, row_token, ring);
   }
 }
 
@@ -602,14 +603,26 @@ __device__ __forceinline__ void fused_dispatch(const GemmParams& p, const RouteP
   __syncthreads();
 }
 
-// PACKED: p.w13 is the packed copy of W13 (moe_fp8_run_packed).
-template <bool PACKED>
+// PACKED: p.w13 is the packed copy of W13 (moe_fp8_run_packed). RING: the depth of the packed
+// instance's register ring (0: StreamShape<kG1>::kRing).
+// Batches of up to kDeepRingTokens tokens take kDeepRing slots (kDeepRing - 1 K-steps in flight
+// per wavefront instead of one): they touch a few experts, so only a few hundred wavefronts
+// stream and each one's depth sets the rate. Measured through the C ABI on seeded batches
+// (two runs each, us per layer, 2 / 3 / 4 slots): T=1 with 2 experts 34.6 / 30.8 / 29.3, T=2
+// with 3 experts 41.2 / 37.5 / 35.8, T=4 with 4 experts 45.0 / 42.1 / 42.5, T=8 with 3 experts
+// 41.6 / 37.7 / 36.2; with 5-6 experts (640-768 units) within +-0.5; at T=16 (10 experts, 1280
+// units) 84.8 / 86.3 / 85.3, hence the bound. Bit-identical to the 2-slot ring.
+constexpr int kDeepRingTokens = 8;
+constexpr int kDeepRing = 4;
+
+template <bool PACKED, int RING = 0>
 __global__ __launch_bounds__(kStreamWaves * 64) void gemm1_stream_dispatch_kernel(GemmParams p, RouteParams rp) {
+  static_assert(RING == 0 || PACKED, "the row-major instance's LDS ring waits assume StreamShape's depth");
   __shared__ __attribute__((aligned(1024))) FusedDispatch<!PACKED> s;
   fused_dispatch(p, rp, s);
   uint8_t* ring = nullptr;
   if constexpr (!PACKED) ring = s.ring[threadIdx.x >> 6];
-  stream_units<kG1, 1, PACKED>(p, s.n_items, s.items, s.row_token, ring);
+  stream_units<kG1, 1, PACKED, RING>(p, s.n_items, s.items, s.row_token, ring);
 }
 
 // Requantises the fp32 SwiGLU rows: per row and COLS columns, scale = max(amax/448, 1e-12)
@@ -1032,13 +1045,17 @@ hipError_t launch_gemm1(const GemmParams& p, int rows_per_item, bool packed, hip
 
 hipError_t launch_gemm1_dispatch(const GemmParams& p, const RouteParams& rp, bool packed, hipStream_t s) {
   // one wave of resident work-groups of the instance launched (each has its own occupancy)
-  static std::atomic<int> occ_rows{0}, occ_packed{0};
+  static std::atomic<int> occ_rows{0}, occ_packed{0}, occ_deep{0};
   if (p.T <= 0 || p.T > kFusedDispatchTokens || rp.rows_per_item != kFusedItemRows) return hipErrorInvalidValue;
-  int grid = num_cus() * (packed ? resident_per_cu(gemm1_stream_dispatch_kernel<true>, occ_packed)
-                                 : resident_per_cu(gemm1_stream_dispatch_kernel<false>, occ_rows));
+  const bool deep = packed && p.T <= kDeepRingTokens;
+  int grid = num_cus() * (deep     ? resident_per_cu(gemm1_stream_dispatch_kernel<true, kDeepRing>, occ_deep)
+                          : packed ? resident_per_cu(gemm1_stream_dispatch_kernel<true>, occ_packed)
+                                   : resident_per_cu(gemm1_stream_dispatch_kernel<false>, occ_rows));
   const int cap = (kFusedItems * StreamShape<kG1>::kSlices + kStreamWaves - 1) / kStreamWaves;
   if (grid > cap) grid = cap;
-  if (packed)
+  if (deep)
+    hipLaunchKernelGGL((gemm1_stream_dispatch_kernel<true, kDeepRing>), dim3(grid), dim3(kStreamWaves * 64), 0, s, p, rp);
+  else if (packed)
     hipLaunchKernelGGL(gemm1_stream_dispatch_kernel<true>, dim3(grid), dim3(kStreamWaves * 64), 0, s, p, rp);
   else
     hipLaunchKernelGGL(gemm1_stream_dispatch_kernel<false>, dim3(grid), dim3(kStreamWaves * 64), 0, s, p, rp);
