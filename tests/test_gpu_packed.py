@@ -80,7 +80,8 @@ def test_packed_copy_is_a_permutation_of_the_weights():
         assert torch.equal(torch.bincount(part.int(), minlength=256), torch.bincount(s.int(), minlength=256))
 
 
-@pytest.mark.parametrize("T,offset,out_dtype", [(1, 0, torch.bfloat16), (16, 0, torch.bfloat16),
+@pytest.mark.parametrize("T,offset,out_dtype", [(1, 0, torch.bfloat16), (4, 224, torch.float32), (8, 0, torch.bfloat16),
+                                                (9, 0, torch.bfloat16), (16, 0, torch.bfloat16),
                                                 (64, 0, torch.bfloat16), (64, 96, torch.bfloat16),
                                                 (40, 224, torch.float32), (65, 0, torch.bfloat16),
                                                 (200, 32, torch.bfloat16), (256, 0, torch.float32), (257, 0, torch.bfloat16),
@@ -90,7 +91,11 @@ def test_run_packed_is_bit_identical_to_run(T, offset, out_dtype):
     dev = torch.device("cuda:0")
     w, packed = _weights_and_packed()
     print(f"run_packed against run: T={T} offset={offset} {out_dtype}", flush=True)
-    logits, bias, hq, hs = gh.inputs.make_activations(T, 6100 + T + offset, dev, local_expert_offset=offset)
+    # up to 8 tokens GEMM1 runs its deep-ring instance; a few boosted local experts make sure
+    # these batches have local work
+    boosted = (1, 7, 12, 30) if T <= 9 else ()
+    logits, bias, hq, hs = gh.inputs.make_activations(T, 6100 + T + offset, dev, local_expert_offset=offset,
+                                                      boosted_local_experts=boosted)
     kw = dict(routing_logits=logits, routing_bias=bias, hidden_states=hq, hidden_states_scale=hs,
               gemm1_weights=w[0], gemm1_weights_scale=w[1], gemm2_weights=w[2], gemm2_weights_scale=w[3],
               local_expert_offset=offset, routed_scaling_factor=2.5)
@@ -100,6 +105,8 @@ def test_run_packed_is_bit_identical_to_run(T, offset, out_dtype):
     gh.pkg.run_packed(**kw, output=got, packed_weights=packed)
     torch.cuda.synchronize()
     assert torch.isfinite(ref).all()
+    if boosted:
+        assert ref.float().abs().amax() > 0
     assert torch.equal(ref.view(torch.int16) if out_dtype == torch.bfloat16 else ref.view(torch.int32),
                        got.view(torch.int16) if out_dtype == torch.bfloat16 else got.view(torch.int32))
 
