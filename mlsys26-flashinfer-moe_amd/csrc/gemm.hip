@@ -605,15 +605,19 @@ __device__ __forceinline__ void fused_dispatch(const GemmParams& p, const RouteP
 
 // PACKED: p.w13 is the packed copy of W13 (moe_fp8_run_packed). RING: the depth of the packed
 // instance's register ring (0: StreamShape<kG1>::kRing).
-// Batches of up to kDeepRingTokens tokens take kDeepRing slots (kDeepRing - 1 K-steps in flight
-// per wavefront instead of one): they touch a few experts, so only a few hundred wavefronts
-// stream and each one's depth sets the rate. Measured through the C ABI on seeded batches
-// (two runs each, us per layer, 2 / 3 / 4 slots): T=1 with 2 experts 34.6 / 30.8 / 29.3, T=2
-// with 3 experts 41.2 / 37.5 / 35.8, T=4 with 4 experts 45.0 / 42.1 / 42.5, T=8 with 3 experts
-// 41.6 / 37.7 / 36.2; with 5-6 experts (640-768 units) within +-0.5; at T=16 (10 experts, 1280
-// units) 84.8 / 86.3 / 85.3, hence the bound. Bit-identical to the 2-slot ring.
+// Small batches take deeper rings (RING - 1 K-steps in flight per wavefront instead of one):
+// they touch a few experts, so only a few hundred wavefronts stream and each one's depth sets
+// the rate. Measured through the C ABI on seeded batches (two runs each, us per layer, 2 / 3 /
+// 4 slots): T=1 with 2 experts 34.6 / 30.8 / 29.3, T=2 with 3 experts 41.2 / 37.5 / 35.8, T=4
+// with 4 experts 45.0 / 42.1 / 42.5, T=8 with 3 experts 41.6 / 37.7 / 36.2; with 5-6 experts
+// (640-768 units) within +-0.5; at T=16 (10 experts, 1280 units) 84.8 / 86.3 / 85.3, hence
+// the bound of 8 tokens. 4 / 6 / 8 slots: 2 experts (256 units) 30.4 / 28.4 / 28.0 and 30.3 /
+// 27.9 / 27.9, 3 experts 36.3 / 35.9 / 36.5, 5 experts 49.9 / 50.8 / 51.7: 6 slots up to 2
+// tokens. Bit-identical to the 2-slot ring.
 constexpr int kDeepRingTokens = 8;
 constexpr int kDeepRing = 4;
+constexpr int kDeeperRingTokens = 2;
+constexpr int kDeeperRing = 6;
 
 template <bool PACKED, int RING = 0>
 __global__ __launch_bounds__(kStreamWaves * 64) void gemm1_stream_dispatch_kernel(GemmParams p, RouteParams rp) {
@@ -1045,15 +1049,19 @@ hipError_t launch_gemm1(const GemmParams& p, int rows_per_item, bool packed, hip
 
 hipError_t launch_gemm1_dispatch(const GemmParams& p, const RouteParams& rp, bool packed, hipStream_t s) {
   // one wave of resident work-groups of the instance launched (each has its own occupancy)
-  static std::atomic<int> occ_rows{0}, occ_packed{0}, occ_deep{0};
+  static std::atomic<int> occ_rows{0}, occ_packed{0}, occ_deep{0}, occ_deeper{0};
   if (p.T <= 0 || p.T > kFusedDispatchTokens || rp.rows_per_item != kFusedItemRows) return hipErrorInvalidValue;
-  const bool deep = packed && p.T <= kDeepRingTokens;
-  int grid = num_cus() * (deep     ? resident_per_cu(gemm1_stream_dispatch_kernel<true, kDeepRing>, occ_deep)
+  const bool deeper = packed && p.T <= kDeeperRingTokens;
+  const bool deep = packed && !deeper && p.T <= kDeepRingTokens;
+  int grid = num_cus() * (deeper   ? resident_per_cu(gemm1_stream_dispatch_kernel<true, kDeeperRing>, occ_deeper)
+                          : deep   ? resident_per_cu(gemm1_stream_dispatch_kernel<true, kDeepRing>, occ_deep)
                           : packed ? resident_per_cu(gemm1_stream_dispatch_kernel<true>, occ_packed)
                                    : resident_per_cu(gemm1_stream_dispatch_kernel<false>, occ_rows));
   const int cap = (kFusedItems * StreamShape<kG1>::kSlices + kStreamWaves - 1) / kStreamWaves;
   if (grid > cap) grid = cap;
-  if (deep)
+  if (deeper)
+    hipLaunchKernelGGL((gemm1_stream_dispatch_kernel<true, kDeeperRing>), dim3(grid), dim3(kStreamWaves * 64), 0, s, p, rp);
+  else if (deep)
     hipLaunchKernelGGL((gemm1_stream_dispatch_kernel<true, kDeepRing>), dim3(grid), dim3(kStreamWaves * 64), 0, s, p, rp);
   else if (packed)
     hipLaunchKernelGGL(gemm1_stream_dispatch_kernel<true>, dim3(grid), dim3(kStreamWaves * 64), 0, s, p, rp);

@@ -80,7 +80,8 @@ def test_packed_copy_is_a_permutation_of_the_weights():
         assert torch.equal(torch.bincount(part.int(), minlength=256), torch.bincount(s.int(), minlength=256))
 
 
-@pytest.mark.parametrize("T,offset,out_dtype", [(1, 0, torch.bfloat16), (4, 224, torch.float32), (8, 0, torch.bfloat16),
+@pytest.mark.parametrize("T,offset,out_dtype", [(1, 0, torch.bfloat16), (2, 32, torch.bfloat16), (3, 0, torch.bfloat16),
+                                                (4, 224, torch.float32), (8, 0, torch.bfloat16),
                                                 (9, 0, torch.bfloat16), (16, 0, torch.bfloat16),
                                                 (64, 0, torch.bfloat16), (64, 96, torch.bfloat16),
                                                 (40, 224, torch.float32), (65, 0, torch.bfloat16),
@@ -91,8 +92,8 @@ def test_run_packed_is_bit_identical_to_run(T, offset, out_dtype):
     dev = torch.device("cuda:0")
     w, packed = _weights_and_packed()
     print(f"run_packed against run: T={T} offset={offset} {out_dtype}", flush=True)
-    # up to 8 tokens GEMM1 runs its deep-ring instance; a few boosted local experts make sure
-    # these batches have local work
+    # up to 8 tokens GEMM1 runs its deep-ring instances (6 slots up to 2 tokens, 4 up to 8); a few
+    # boosted local experts make sure these batches have local work
     boosted = (1, 7, 12, 30) if T <= 9 else ()
     logits, bias, hq, hs = gh.inputs.make_activations(T, 6100 + T + offset, dev, local_expert_offset=offset,
                                                       boosted_local_experts=boosted)
