@@ -49,7 +49,9 @@ constexpr int kStreamWaves = 4;                      // wavefronts per work-grou
 //   GEMM1: a unit is 16 SwiGLU columns = their 16 gate rows + 16 up rows (2 fragments).
 //   GEMM2: a unit is 64 hidden rows (4 fragments).
 // Both use a 2-slot ring (one K-step in flight per wavefront besides the one consumed; GEMM1
-// 96 registers with the accumulators, GEMM2 136), so that at decode sizes every unit has its own
+// 96 registers with the accumulators, GEMM2 136; batches of up to 8 tokens, whose few units
+// leave most wavefront slots empty, stream GEMM1's packed copy through 4 or 6 slots, see
+// gemm1_stream_dispatch_kernel), so that at decode sizes every unit has its own
 // wavefront and the grid drains in one round. The whole chip then keeps ~15 MB of weight loads
 // in flight; a plain HBM read peaks at 6-8 MB in flight and slows beyond. Measured at T=64:
 // GEMM1 117 -> 109 us and GEMM2 64 -> 57 us against 4-slot rings and 32-row GEMM2 units; GEMM1
