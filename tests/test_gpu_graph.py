@@ -16,13 +16,16 @@ def _gh():
     return gpu_helpers
 
 
-@pytest.mark.parametrize("T", [48, 700])   # decode path (stream GEMMs) and tile path
+# decode path (stream GEMMs; at T=2 GEMM1's 6-slot ring, boosted local experts giving it work)
+# and tile path
+@pytest.mark.parametrize("T", [2, 48, 700])
 def test_graph_replays_match_eager(T):
     gh = _gh()
     dev = torch.device("cuda:0")
     torch.manual_seed(T)
     w = gh.inputs.make_weights(31 + T, dev)
-    logits, bias, hq, hs = gh.inputs.make_activations(T, 500 + T, dev)
+    boosted = (1, 7, 12, 30) if T <= 8 else ()
+    logits, bias, hq, hs = gh.inputs.make_activations(T, 500 + T, dev, boosted_local_experts=boosted)
     kw = dict(routing_logits=logits, routing_bias=bias, hidden_states=hq, hidden_states_scale=hs,
               gemm1_weights=w[0], gemm1_weights_scale=w[1], gemm2_weights=w[2], gemm2_weights_scale=w[3],
               local_expert_offset=0, routed_scaling_factor=2.5)
