@@ -606,7 +606,7 @@ __device__ __forceinline__ void fused_dispatch(const GemmParams& p, const RouteP
 }
 
 // PACKED: p.w13 is the packed copy of W13 (moe_fp8_run_packed). RING: the depth of the packed
-// instance's register ring (0: StreamShape<kG1>::kRing).
+// instance's register ring (0: StreamShape<kG1>::kRing; gemm1_stream_dispatch_deep_kernel).
 // Small batches take deeper rings (RING - 1 K-steps in flight per wavefront instead of one):
 // they touch a few experts, so only a few hundred wavefronts stream and each one's depth sets
 // the rate. Measured through the C ABI on seeded batches (two runs each, us per layer, 2 / 3 /
@@ -621,14 +621,25 @@ constexpr int kDeepRing = 4;
 constexpr int kDeeperRingTokens = 2;
 constexpr int kDeeperRing = 6;
 
-template <bool PACKED, int RING = 0>
-__global__ __launch_bounds__(kStreamWaves * 64) void gemm1_stream_dispatch_kernel(GemmParams p, RouteParams rp) {
+template <bool PACKED, int RING>
+__device__ __forceinline__ void gemm1_stream_dispatch(const GemmParams& p, const RouteParams& rp) {
   static_assert(RING == 0 || PACKED, "the row-major instance's LDS ring waits assume StreamShape's depth");
   __shared__ __attribute__((aligned(1024))) FusedDispatch<!PACKED> s;
   fused_dispatch(p, rp, s);
   uint8_t* ring = nullptr;
   if constexpr (!PACKED) ring = s.ring[threadIdx.x >> 6];
   stream_units<kG1, 1, PACKED, RING>(p, s.n_items, s.items, s.row_token, ring);
+}
+
+template <bool PACKED>
+__global__ __launch_bounds__(kStreamWaves * 64) void gemm1_stream_dispatch_kernel(GemmParams p, RouteParams rp) {
+  gemm1_stream_dispatch<PACKED, 0>(p, rp);
+}
+
+// The packed instance on a RING-slot register ring (batches of up to kDeepRingTokens tokens).
+template <int RING>
+__global__ __launch_bounds__(kStreamWaves * 64) void gemm1_stream_dispatch_deep_kernel(GemmParams p, RouteParams rp) {
+  gemm1_stream_dispatch<true, RING>(p, rp);
 }
 
 // Requantises the fp32 SwiGLU rows: per row and COLS columns, scale = max(amax/448, 1e-12)
@@ -1055,16 +1066,16 @@ hipError_t launch_gemm1_dispatch(const GemmParams& p, const RouteParams& rp, boo
   if (p.T <= 0 || p.T > kFusedDispatchTokens || rp.rows_per_item != kFusedItemRows) return hipErrorInvalidValue;
   const bool deeper = packed && p.T <= kDeeperRingTokens;
   const bool deep = packed && !deeper && p.T <= kDeepRingTokens;
-  int grid = num_cus() * (deeper   ? resident_per_cu(gemm1_stream_dispatch_kernel<true, kDeeperRing>, occ_deeper)
-                          : deep   ? resident_per_cu(gemm1_stream_dispatch_kernel<true, kDeepRing>, occ_deep)
+  int grid = num_cus() * (deeper   ? resident_per_cu(gemm1_stream_dispatch_deep_kernel<kDeeperRing>, occ_deeper)
+                          : deep   ? resident_per_cu(gemm1_stream_dispatch_deep_kernel<kDeepRing>, occ_deep)
                           : packed ? resident_per_cu(gemm1_stream_dispatch_kernel<true>, occ_packed)
                                    : resident_per_cu(gemm1_stream_dispatch_kernel<false>, occ_rows));
   const int cap = (kFusedItems * StreamShape<kG1>::kSlices + kStreamWaves - 1) / kStreamWaves;
   if (grid > cap) grid = cap;
   if (deeper)
-    hipLaunchKernelGGL((gemm1_stream_dispatch_kernel<true, kDeeperRing>), dim3(grid), dim3(kStreamWaves * 64), 0, s, p, rp);
+    hipLaunchKernelGGL(gemm1_stream_dispatch_deep_kernel<kDeeperRing>, dim3(grid), dim3(kStreamWaves * 64), 0, s, p, rp);
   else if (deep)
-    hipLaunchKernelGGL((gemm1_stream_dispatch_kernel<true, kDeepRing>), dim3(grid), dim3(kStreamWaves * 64), 0, s, p, rp);
+    hipLaunchKernelGGL(gemm1_stream_dispatch_deep_kernel<kDeepRing>, dim3(grid), dim3(kStreamWaves * 64), 0, s, p, rp);
   else if (packed)
     hipLaunchKernelGGL(gemm1_stream_dispatch_kernel<true>, dim3(grid), dim3(kStreamWaves * 64), 0, s, p, rp);
   else
