@@ -673,12 +673,12 @@ __global__ __launch_bounds__(256) void requant_kernel(GemmParams p) {
 // one kernel, with no fp32 rows parked in `partial`. A work-group owns 28 hidden rows of W2
 // (256 slices, one per CU: two MFMA fragments, the second's last four rows repeating its last
 // row and never stored) across every work item, and its wavefront q owns K-steps
-// [4q, 4q+4) of each: per item, q streams the expert's 32 x 512 weight bytes and the item's
+// [2q, 2q+2) of each: per item, q streams the expert's 32 x 256 weight bytes and the item's
 // act rows through a register ring, scales each 128-wide block product (kernel.py:234),
 // weights it by the routing weight (kernel.py:236-237) and adds it into its own LDS
 // accumulator of (token, hidden row). Items come in expert order, so each token's
 // contributions are added in ascending local expert order, and the rows of one token inside
-// an item (a repeated expert id) in slot order; the work-group then sums its four K quarters
+// an item (a repeated expert id) in slot order; the work-group then sums its eight K parts
 // in fixed order and writes the 28 columns of every token, zeros for tokens without a local
 // expert (the zero-fill and finalize of kernel.py:704, 729). Deterministic, no atomics.
 // 28-row slices against 32-row ones (224 work-groups, 32 CUs idle): every output element is
@@ -690,10 +690,13 @@ __global__ __launch_bounds__(256) void requant_kernel(GemmParams p) {
 // wavefront-per-unit GEMM2 plus combine_kernel. One fragment spends a 2 KB activation
 // fragment and four small loads on every 2 KB of weights; four need more registers than two
 // wavefronts per SIMD allow, and one wavefront per SIMD cannot keep the matrix core busy.
+// Eight wavefronts of 2 K-steps per item (two per SIMD, 180 registers) against four of 4 (one
+// per SIMD, 240): GEMM2 stage 56.7-56.8 -> 55.9-56.6 us at T=64, 32.4-32.6 -> 32.0-32.2 at T=16
+// (four runs each); the K parts' sum changes order, within the parity bounds.
 constexpr int kSliceF = 2;                               // weight fragments per wavefront
 constexpr int kSliceRows = 28;                           // hidden rows per work-group
-constexpr int kSliceQuarters = 4;                        // wavefronts per work-group = K quarters
-constexpr int kSliceSteps = kIBlocks / kSliceQuarters;   // 4 K-steps per quarter and item
+constexpr int kSliceParts = 8;                           // wavefronts per work-group = K parts
+constexpr int kSliceSteps = kIBlocks / kSliceParts;      // 2 K-steps per part and item
 constexpr int kSliceRing = 2;                            // ring slots: 1 step in flight besides the one consumed
 constexpr int kHiddenSlices = kHidden / kSliceRows;      // 256
 static_assert(kHidden % kSliceRows == 0 && kSliceRows > 16 * (kSliceF - 1) && kSliceRows <= 16 * kSliceF,
@@ -722,13 +725,13 @@ constexpr int kSliceLdsDma = kSliceLdsRows / 8;                 // 4 DMA instruc
 
 template <bool RING>
 struct SliceShared {
-  float acc[kSliceQuarters][kFusedDispatchTokens][16 * kSliceF];
-  uint8_t ring[RING ? kSliceQuarters : 0][kSliceRing * kSliceLdsStep];
+  float acc[kSliceParts][kFusedDispatchTokens][16 * kSliceF];
+  uint8_t ring[RING ? kSliceParts : 0][kSliceRing * kSliceLdsStep];
 };
 
 // PACKED: p.w2 is the packed copy of W2 (moe_fp8_run_packed).
 template <bool PACKED>
-__global__ __launch_bounds__(kSliceQuarters * 64) void gemm2_slice_kernel(GemmParams p) {
+__global__ __launch_bounds__(kSliceParts * 64) void gemm2_slice_kernel(GemmParams p) {
   __shared__ __attribute__((aligned(1024))) SliceShared<!PACKED> sh;
   auto& acc_lds = sh.acc;
   const int lane = threadIdx.x & 63;
@@ -876,14 +879,14 @@ __global__ __launch_bounds__(kSliceQuarters * 64) void gemm2_slice_kernel(GemmPa
       if constexpr (!PACKED) wait_vm<0>();
     }
     __syncthreads();
-    // the four K quarters, summed in fixed order: 4 columns of one token per thread (the slice's
+    // the K parts, summed in fixed order: 4 columns of one token per thread (the slice's
     // 28 columns; the accumulators' last 4 hold the repeated rows)
     constexpr int kChunks = kSliceRows / 4;
-    for (int i = threadIdx.x; i < T * kChunks; i += kSliceQuarters * 64) {
+    for (int i = threadIdx.x; i < T * kChunks; i += kSliceParts * 64) {
       const int t = i / kChunks, c = 4 * (i % kChunks);
-      const v4f s = ((*reinterpret_cast<const v4f*>(&acc_lds[0][t][c]) + *reinterpret_cast<const v4f*>(&acc_lds[1][t][c])) +
-                     *reinterpret_cast<const v4f*>(&acc_lds[2][t][c])) +
-                    *reinterpret_cast<const v4f*>(&acc_lds[3][t][c]);
+      v4f s = *reinterpret_cast<const v4f*>(&acc_lds[0][t][c]);
+#pragma unroll
+      for (int qq = 1; qq < kSliceParts; ++qq) s += *reinterpret_cast<const v4f*>(&acc_lds[qq][t][c]);
       const size_t o = (size_t)t * kHidden + h0 + c;
       if (p.out_dtype == MOE_FP8_OUT_BF16)
         *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(p.out) + o) = pack_bf16x4(s[0], s[1], s[2], s[3]);
@@ -1099,8 +1102,8 @@ hipError_t launch_gemm2(const GemmParams& p, int rows_per_item, bool packed, hip
   if (rows_per_item == kFusedItemRows) {
     // up to 64 tokens: GEMM2 with the combine, one work-group per 32-row hidden slice
     if (p.T > kFusedDispatchTokens) return hipErrorInvalidValue;
-    if (packed) hipLaunchKernelGGL(gemm2_slice_kernel<true>, dim3(kHiddenSlices), dim3(kSliceQuarters * 64), 0, s, p);
-    else hipLaunchKernelGGL(gemm2_slice_kernel<false>, dim3(kHiddenSlices), dim3(kSliceQuarters * 64), 0, s, p);
+    if (packed) hipLaunchKernelGGL(gemm2_slice_kernel<true>, dim3(kHiddenSlices), dim3(kSliceParts * 64), 0, s, p);
+    else hipLaunchKernelGGL(gemm2_slice_kernel<false>, dim3(kHiddenSlices), dim3(kSliceParts * 64), 0, s, p);
     return hipGetLastError();
   }
   return launch_stream<kG2>(p, rows_per_item, packed, s);
